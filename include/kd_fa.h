@@ -1,0 +1,202 @@
+/*
+ * kd_fa.h - C ABI of the gfx950 flash-attention backend hook for
+ *           kandinsky.cpp's CrossDiT attention (GGML_OP_FLASH_ATTN_EXT).
+ *
+ * The reference builds exactly one flash-attention node:
+ *     kqv = ggml_flash_attn_ext(ctx, q, k, v_perm, mask_f16, scale, 0, 0);
+ *     ggml_flash_attn_ext_set_prec(kqv, GGML_PREC_F32);
+ * (src/core/ops.hpp:176-177), asks the backend whether it can run it
+ * (ggml_backend_supports_op, src/core/ops.hpp:179) and executes it inside
+ * ggml_backend_graph_compute (src/core/executor.hpp:241).  This header is
+ * the drop-in for that one node: kd_fa_supports replaces the supports_op
+ * answer for GGML_OP_FLASH_ATTN_EXT, kd_fa_run replaces the backend's
+ * kernel for the node, and kd_fa_rope_run additionally fuses the
+ * rope::apply rotation of Q and K (src/rope.hpp:109-155, called at
+ * src/models/crossdit.hpp:139-142) into the operand loads.
+ *
+ * Tensor views follow ggml's model: ne[0] is the innermost (contiguous)
+ * dimension, nb[] are byte strides, type ids are ggml's ggml_type values,
+ * so a ggml adaptor passes tensor->type / ne / nb / data through unchanged.
+ *
+ * Op contract (ggml GGML_OP_FLASH_ATTN_EXT, as ops.hpp:122-183 builds it):
+ *   q    [Dk, Lq, H,   B ]  F32, F16 or BF16 (converted to K's type)
+ *   k    [Dk, Lk, Hkv, Bk]  F16 or BF16
+ *   v    [Dv, Lk, Hkv, Bk]  same type as k (not transposed)
+ *   mask [Lk', Lq', Hm, Bm] F16, optional; Lk' >= Lk, Lq' >= Lq,
+ *                           broadcast over heads (H % Hm == 0) and
+ *                           batch (B % Bm == 0); row of query i is ne1 = i
+ *   dst  [Dv, H, Lq, B]     F32, contiguous (ggml's permuted result)
+ *   dst[b][i][h][:] = sum_j softmax_j(scale * <q_bhi, k_j> + mask[b,h,i,j]) v_j
+ *   with h_kv = h / (H / Hkv) and b_kv = b / (B / Bk).  A row whose keys
+ *   are all masked (-inf) is written as zeros.
+ *
+ * All device pointers belong to the caller; no entry point allocates,
+ * frees, synchronises or retains a pointer.  Work is enqueued on the given
+ * HIP stream (NULL = the legacy default stream).
+ */
+#ifndef KD_FA_H
+#define KD_FA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml_type ids (ggml.h enum ggml_type) for the types this op accepts. */
+enum {
+    KD_FA_TYPE_F32  = 0,
+    KD_FA_TYPE_F16  = 1,
+    KD_FA_TYPE_BF16 = 30
+};
+
+/* ggml_prec (ggml.h enum ggml_prec). */
+enum {
+    KD_FA_PREC_DEFAULT = 0,
+    KD_FA_PREC_F32     = 10
+};
+
+/* Status codes.  Every entry point returns one of these; none aborts. */
+enum {
+    KD_FA_OK             = 0,
+    KD_FA_ERR_NULL       = -1,   /* NULL descriptor or data pointer       */
+    KD_FA_ERR_TYPE       = -2,   /* unsupported tensor type               */
+    KD_FA_ERR_SHAPE      = -3,   /* shapes inconsistent with the op       */
+    KD_FA_ERR_LAYOUT     = -4,   /* stride / alignment not supported      */
+    KD_FA_ERR_PARAM      = -5,   /* max_bias, softcap or scale unsupported */
+    KD_FA_ERR_ROPE       = -6,   /* invalid RoPE descriptor               */
+    KD_FA_ERR_LAUNCH     = -7,   /* HIP launch failed                     */
+    KD_FA_ERR_DEVICE     = -8    /* no gfx950 device / runtime error      */
+};
+
+/* A ggml tensor view: struct ggml_tensor's type, ne, nb and data. */
+typedef struct kd_fa_tensor {
+    int32_t type;
+    int64_t ne[4];
+    size_t  nb[4];
+    void   *data;
+} kd_fa_tensor;
+
+/*
+ * The GGML_OP_FLASH_ATTN_EXT node: src[0..3] = q, k, v, mask and the op
+ * params {scale, max_bias, logit_softcap, prec}
+ * (ggml_flash_attn_ext + ggml_flash_attn_ext_set_prec, ops.hpp:176-177).
+ * mask.data == NULL means "no mask" (ops.hpp:171-174 passes nullptr).
+ */
+typedef struct kd_fa_desc {
+    kd_fa_tensor q;
+    kd_fa_tensor k;
+    kd_fa_tensor v;
+    kd_fa_tensor mask;
+    kd_fa_tensor dst;
+    float   scale;
+    float   max_bias;
+    float   logit_softcap;
+    int32_t prec;
+} kd_fa_desc;
+
+/* RoPE operand rotation modes for kd_fa_rope_run. */
+enum {
+    KD_FA_ROPE_NONE  = 0,
+    /* table: F32 [D, L'] view with interleaved (cos_i, sin_i) pairs, one
+     * row per token, shared by all heads and batches -- exactly the
+     * rope_cos_sin tensor that rope::apply consumes (src/rope.hpp:109-111)
+     * and compute_visual_rope / compute_text_rope fill
+     * (src/rope.hpp:36-102).  Token i of Q and of K uses row i.          */
+    KD_FA_ROPE_TABLE = 1,
+    /* axes: the same values factorised per axis of a (T, Hp, Wp) token
+     * grid (src/rope.hpp:56-102): a contiguous F32 buffer holding
+     * [T][axes[0]] ++ [Hp][axes[1]] ++ [Wp][axes[2]] interleaved
+     * (cos, sin) pairs, built by kd_fa_rope_axes_fill.  Token index
+     * idx = (t*Hp + h)*Wp + w (rope.hpp:74).                             */
+    KD_FA_ROPE_AXES  = 2
+};
+
+typedef struct kd_fa_rope {
+    int32_t      mode;
+    kd_fa_tensor table;      /* KD_FA_ROPE_TABLE                         */
+    const float *axes_data;  /* KD_FA_ROPE_AXES: device pointer           */
+    int32_t      grid[3];    /* KD_FA_ROPE_AXES: T, Hp, Wp                */
+    int32_t      axes[3];    /* KD_FA_ROPE_AXES: per-axis dims, sum = Dk  */
+} kd_fa_rope;
+
+/*
+ * kd_fa_supports - replaces ggml_backend_supports_op for the node
+ * (src/core/ops.hpp:179).  Returns 1 when kd_fa_run can execute it, 0 when
+ * the caller must take its fallback (ops.hpp:187-202).  Host-only: never
+ * touches the GPU.  When the answer is 0 and reason != NULL, *reason gets
+ * the KD_FA_ERR_* code naming the first failed condition.
+ */
+int kd_fa_supports(const kd_fa_desc *desc, int *reason);
+
+/*
+ * kd_fa_run - executes the GGML_OP_FLASH_ATTN_EXT node on a gfx950 GPU,
+ * replacing the backend kernel that ggml_backend_graph_compute dispatches
+ * for it (src/core/executor.hpp:241; node built at src/core/ops.hpp:176).
+ * Asynchronous on `stream` (a hipStream_t).  Returns KD_FA_OK or a
+ * negative KD_FA_ERR_* code; on error nothing is enqueued.
+ */
+int kd_fa_run(const kd_fa_desc *desc, void *stream);
+
+/*
+ * kd_fa_rope_run - rope::apply(q), rope::apply(k) (src/rope.hpp:109-155,
+ * as DiTSelfAttention::forward calls it, src/models/crossdit.hpp:139-142)
+ * fused into kd_fa_run.  The result is defined as kd_fa_run on
+ * q' = round_K(rot(q)), k' = round_K(rot(k)): each interleaved pair
+ * (x0, x1) = (x[2i], x[2i+1]) of a token's row becomes
+ * (x0*c - x1*s, x0*s + x1*c) in F32, then is rounded to K's type
+ * (round to nearest even), as if the caller had materialised rope::apply's
+ * F32 output and cast it to K's type (src/core/ops.hpp:167).
+ * rope == NULL or mode KD_FA_ROPE_NONE is kd_fa_run.
+ */
+int kd_fa_rope_run(const kd_fa_desc *desc, const kd_fa_rope *rope, void *stream);
+
+/*
+ * kd_fa_rope_supports - kd_fa_supports plus the checks of the RoPE
+ * descriptor.  Host-only.
+ */
+int kd_fa_rope_supports(const kd_fa_desc *desc, const kd_fa_rope *rope, int *reason);
+
+/*
+ * kd_fa_rope_visual_table - host-side mirror of rope::compute_visual_rope
+ * (src/rope.hpp:56-102, with get_freqs src/rope.hpp:23-29): fills
+ * out[(t*Hp + h)*Wp + w][Dk] (Dk = sum of axes) with interleaved
+ * (cos, sin) pairs of pos * freq_i / scale_factor[axis].  The values are
+ * computed in F32 exactly as the reference computes them.  Returns
+ * KD_FA_OK or KD_FA_ERR_ROPE.
+ */
+int kd_fa_rope_visual_table(int T, int Hp, int Wp, const int axes[3],
+                            const float scale_factor[3], float theta,
+                            float *out);
+
+/*
+ * kd_fa_rope_axes_size / kd_fa_rope_axes_fill - the factorised form of
+ * the same table for KD_FA_ROPE_AXES: (T*axes[0] + Hp*axes[1] +
+ * Wp*axes[2]) floats, whose entries are bitwise equal to the columns of
+ * kd_fa_rope_visual_table's rows.  Host buffers; the caller copies the
+ * result to the device.
+ */
+size_t kd_fa_rope_axes_size(int T, int Hp, int Wp, const int axes[3]);
+int kd_fa_rope_axes_fill(int T, int Hp, int Wp, const int axes[3],
+                         const float scale_factor[3], float theta,
+                         float *out);
+
+/*
+ * kd_fa_rope_text_table - host-side mirror of rope::compute_text_rope
+ * (src/rope.hpp:36-49), the 1-D table TextBlock self-attention rotates
+ * with: out[pos][D] interleaved (cos, sin) of pos * freq_i.
+ */
+int kd_fa_rope_text_table(int L, int D, float theta, float *out);
+
+/* Human-readable text for a KD_FA_* status code. */
+const char *kd_fa_strerror(int status);
+
+/* Library version, as MAJOR*10000 + MINOR*100 + PATCH. */
+int kd_fa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KD_FA_H */

@@ -1,0 +1,285 @@
+// kd_fa_host.cpp - C ABI of libkd_fa.so (include/kd_fa.h): operator
+// validation (the supports_op answer), RoPE table helpers and the launch of
+// the gfx950 kernels.  Nothing here allocates device memory, synchronises or
+// keeps pointers past the call.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "../../include/kd_fa.h"
+#include "kd_fa_kernel.h"
+
+namespace {
+
+constexpr int64_t kHeadDim = 128;
+constexpr int64_t kI32Max = 0x7fffffff;
+
+size_t elem_size(int type) { return type == KD_FA_TYPE_F32 ? 4 : 2; }
+bool is_16b(uint64_t x) { return (x & 15u) == 0; }
+bool is_16b(const void *p) { return is_16b(reinterpret_cast<uintptr_t>(p)); }
+
+// Conditions of kd_fa_supports.  `mask_vec` reports whether the mask rows
+// can be read 16 bytes at a time.
+int validate(const kd_fa_desc *d, const kd_fa_rope *r, bool *mask_vec) {
+    if (!d) return KD_FA_ERR_NULL;
+    const kd_fa_tensor &q = d->q, &k = d->k, &v = d->v, &m = d->mask, &o = d->dst;
+    if (!q.data || !k.data || !v.data || !o.data) return KD_FA_ERR_NULL;
+
+    // types: Q is converted to K's type on load; K and V share one MFMA type
+    if (q.type != KD_FA_TYPE_F32 && q.type != KD_FA_TYPE_F16 && q.type != KD_FA_TYPE_BF16) return KD_FA_ERR_TYPE;
+    if (k.type != KD_FA_TYPE_F16 && k.type != KD_FA_TYPE_BF16) return KD_FA_ERR_TYPE;
+    if (v.type != k.type) return KD_FA_ERR_TYPE;
+    if (o.type != KD_FA_TYPE_F32) return KD_FA_ERR_TYPE;
+    if (m.data && m.type != KD_FA_TYPE_F16) return KD_FA_ERR_TYPE;
+
+    // op params: plain softmax attention only (ops.hpp:176 passes 0, 0)
+    if (d->max_bias != 0.0f || d->logit_softcap != 0.0f) return KD_FA_ERR_PARAM;
+    if (!std::isfinite(d->scale)) return KD_FA_ERR_PARAM;
+
+    // shapes
+    for (int i = 0; i < 4; ++i)
+        if (q.ne[i] < 0 || k.ne[i] < 0 || v.ne[i] < 0 || o.ne[i] < 0) return KD_FA_ERR_SHAPE;
+    if (q.ne[0] != kHeadDim || k.ne[0] != kHeadDim || v.ne[0] != kHeadDim) return KD_FA_ERR_SHAPE;
+    const int64_t Lq = q.ne[1], Lk = k.ne[1], H = q.ne[2], B = q.ne[3];
+    if (v.ne[1] != Lk) return KD_FA_ERR_SHAPE;
+    if (k.ne[2] == 0 || v.ne[2] == 0 || k.ne[3] == 0 || v.ne[3] == 0) return KD_FA_ERR_SHAPE;
+    if (H % k.ne[2] || H % v.ne[2] || B % k.ne[3] || B % v.ne[3]) return KD_FA_ERR_SHAPE;
+    if (o.ne[0] != v.ne[0] || o.ne[1] != H || o.ne[2] != Lq || o.ne[3] != B) return KD_FA_ERR_SHAPE;
+    if (Lq > kI32Max || Lk > kI32Max || H > kI32Max || B > kI32Max) return KD_FA_ERR_SHAPE;
+    const int64_t n_qt = (Lq + kdfa::kBlockM - 1) / kdfa::kBlockM;
+    if (H > 0 && B > 0 && n_qt > kI32Max / H / B) return KD_FA_ERR_SHAPE;
+    if (m.data) {
+        if (m.ne[0] < Lk || m.ne[1] < Lq || m.ne[2] <= 0 || m.ne[3] <= 0) return KD_FA_ERR_SHAPE;
+        if (H % m.ne[2] || B % m.ne[3]) return KD_FA_ERR_SHAPE;
+    }
+
+    // layouts: unit element stride; 16-byte rows for Q/K/V/dst vector access
+    const kd_fa_tensor *vec_t[4] = {&q, &k, &v, &o};
+    for (const kd_fa_tensor *t : vec_t) {
+        if (t->nb[0] != elem_size(t->type)) return KD_FA_ERR_LAYOUT;
+        if (!is_16b(t->data) || !is_16b(t->nb[1]) || !is_16b(t->nb[2]) || !is_16b(t->nb[3])) return KD_FA_ERR_LAYOUT;
+    }
+    bool mv = false;
+    if (m.data) {
+        if (m.nb[0] != 2) return KD_FA_ERR_LAYOUT;
+        if ((reinterpret_cast<uintptr_t>(m.data) | m.nb[1] | m.nb[2] | m.nb[3]) & 1u) return KD_FA_ERR_LAYOUT;
+        mv = is_16b(m.data) && is_16b(m.nb[1]) && is_16b(m.nb[2]) && is_16b(m.nb[3]);
+    }
+    if (mask_vec) *mask_vec = mv;
+
+    // RoPE
+    if (r && r->mode != KD_FA_ROPE_NONE) {
+        const int64_t L = Lq > Lk ? Lq : Lk;
+        if (r->mode == KD_FA_ROPE_TABLE) {
+            const kd_fa_tensor &t = r->table;
+            if (!t.data || t.type != KD_FA_TYPE_F32) return KD_FA_ERR_ROPE;
+            if (t.ne[0] != kHeadDim || t.ne[1] < L || t.nb[0] != 4) return KD_FA_ERR_ROPE;
+            if (!is_16b(t.data) || !is_16b(t.nb[1])) return KD_FA_ERR_ROPE;
+        } else if (r->mode == KD_FA_ROPE_AXES) {
+            if (!r->axes_data || !is_16b(r->axes_data)) return KD_FA_ERR_ROPE;
+            for (int i = 0; i < 3; ++i) {
+                if (r->axes[i] < 0 || r->axes[i] % 8) return KD_FA_ERR_ROPE;
+                if (r->grid[i] <= 0) return KD_FA_ERR_ROPE;
+            }
+            if (r->axes[0] + r->axes[1] + r->axes[2] != kHeadDim) return KD_FA_ERR_ROPE;
+            const int64_t cells = (int64_t)r->grid[0] * r->grid[1] * r->grid[2];
+            if (cells < L || cells > kI32Max) return KD_FA_ERR_ROPE;
+        } else {
+            return KD_FA_ERR_ROPE;
+        }
+    }
+    return KD_FA_OK;
+}
+
+// gfx950 check, once per device.
+std::atomic<int> g_dev_state[64];
+
+int device_ok() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return KD_FA_ERR_DEVICE;
+    if (dev < 0 || dev >= 64) return KD_FA_ERR_DEVICE;
+    int st = g_dev_state[dev].load(std::memory_order_acquire);
+    if (st == 0) {
+        hipDeviceProp_t prop;
+        st = -1;
+        if (hipGetDeviceProperties(&prop, dev) == hipSuccess &&
+            std::strncmp(prop.gcnArchName, "gfx950", 6) == 0)
+            st = 1;
+        g_dev_state[dev].store(st, std::memory_order_release);
+    }
+    return st == 1 ? KD_FA_OK : KD_FA_ERR_DEVICE;
+}
+
+int run(const kd_fa_desc *d, const kd_fa_rope *r, void *stream) {
+    bool mask_vec = false;
+    int st = validate(d, r, &mask_vec);
+    if (st != KD_FA_OK) return st;
+    const int64_t Lq = d->q.ne[1], H = d->q.ne[2], B = d->q.ne[3];
+    if (Lq == 0 || H == 0 || B == 0) return KD_FA_OK;
+    st = device_ok();
+    if (st != KD_FA_OK) return st;
+
+    kdfa::Args a;
+    std::memset(&a, 0, sizeof(a));
+    a.q = static_cast<const char *>(d->q.data);
+    a.k = static_cast<const char *>(d->k.data);
+    a.v = static_cast<const char *>(d->v.data);
+    a.m = static_cast<const char *>(d->mask.data);
+    a.o = static_cast<char *>(d->dst.data);
+    a.q_nb1 = d->q.nb[1]; a.q_nb2 = d->q.nb[2]; a.q_nb3 = d->q.nb[3];
+    a.k_nb1 = d->k.nb[1]; a.k_nb2 = d->k.nb[2]; a.k_nb3 = d->k.nb[3];
+    a.v_nb1 = d->v.nb[1]; a.v_nb2 = d->v.nb[2]; a.v_nb3 = d->v.nb[3];
+    if (a.m) {
+        a.m_nb1 = d->mask.nb[1]; a.m_nb2 = d->mask.nb[2]; a.m_nb3 = d->mask.nb[3];
+        a.m_ne2 = (int32_t)d->mask.ne[2]; a.m_ne3 = (int32_t)d->mask.ne[3];
+    }
+    a.o_nb1 = d->dst.nb[1]; a.o_nb2 = d->dst.nb[2]; a.o_nb3 = d->dst.nb[3];
+    a.Lq = (int32_t)Lq;
+    a.Lk = (int32_t)d->k.ne[1];
+    a.H = (int32_t)H;
+    a.B = (int32_t)B;
+    a.rk2 = (int32_t)(H / d->k.ne[2]); a.rk3 = (int32_t)(B / d->k.ne[3]);
+    a.rv2 = (int32_t)(H / d->v.ne[2]); a.rv3 = (int32_t)(B / d->v.ne[3]);
+    a.q_type = d->q.type;
+    a.mask_vec = mask_vec ? 1 : 0;
+    a.scale_log2 = d->scale * 1.4426950408889634f;
+    a.rope_mode = r ? r->mode : KD_FA_ROPE_NONE;
+    if (a.rope_mode == KD_FA_ROPE_TABLE) {
+        a.rope_tab = static_cast<const float *>(r->table.data);
+        a.rope_nb1 = (int64_t)r->table.nb[1];
+    } else if (a.rope_mode == KD_FA_ROPE_AXES) {
+        a.axes = r->axes_data;
+        a.grid_t = r->grid[0]; a.grid_h = r->grid[1]; a.grid_w = r->grid[2];
+        a.axis0 = r->axes[0]; a.axis1 = r->axes[1]; a.axis2 = r->axes[2];
+    }
+    a.n_qt = (int32_t)((Lq + kdfa::kBlockM - 1) / kdfa::kBlockM);
+    a.n_blocks = (int32_t)(a.n_qt * H * B);
+
+    if (kdfa::launch(a, d->k.type, static_cast<hipStream_t>(stream)) != hipSuccess) return KD_FA_ERR_LAUNCH;
+    return KD_FA_OK;
+}
+
+// rope::get_freqs (src/rope.hpp:23-29), same float expression order.
+void rope_freqs(int dim, float max_period, float *out) {
+    for (int i = 0; i < dim; i++) out[i] = expf(-logf(max_period) * (float)i / (float)dim);
+}
+
+bool axes_ok(int T, int Hp, int Wp, const int axes[3]) {
+    if (!axes || T <= 0 || Hp <= 0 || Wp <= 0) return false;
+    for (int i = 0; i < 3; ++i)
+        if (axes[i] < 0 || axes[i] % 2) return false;
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kd_fa_supports(const kd_fa_desc *desc, int *reason) {
+    const int st = validate(desc, nullptr, nullptr);
+    if (reason) *reason = st;
+    return st == KD_FA_OK ? 1 : 0;
+}
+
+int kd_fa_rope_supports(const kd_fa_desc *desc, const kd_fa_rope *rope, int *reason) {
+    const int st = validate(desc, rope, nullptr);
+    if (reason) *reason = st;
+    return st == KD_FA_OK ? 1 : 0;
+}
+
+int kd_fa_run(const kd_fa_desc *desc, void *stream) { return run(desc, nullptr, stream); }
+
+int kd_fa_rope_run(const kd_fa_desc *desc, const kd_fa_rope *rope, void *stream) {
+    return run(desc, rope, stream);
+}
+
+// rope::compute_visual_rope (src/rope.hpp:56-102).
+int kd_fa_rope_visual_table(int T, int Hp, int Wp, const int axes[3], const float sf[3],
+                            float theta, float *out) {
+    if (!axes_ok(T, Hp, Wp, axes) || !sf || !out) return KD_FA_ERR_ROPE;
+    const int D = axes[0] + axes[1] + axes[2];
+    std::vector<float> f[3];
+    for (int a = 0; a < 3; ++a) {
+        f[a].resize(axes[a] / 2 + 1);
+        rope_freqs(axes[a] / 2, theta, f[a].data());
+    }
+    for (int t = 0; t < T; t++)
+        for (int h = 0; h < Hp; h++)
+            for (int w = 0; w < Wp; w++) {
+                float *row = out + (size_t)((t * Hp + h) * Wp + w) * D;
+                const int pos[3] = {t, h, w};
+                int off = 0;
+                for (int a = 0; a < 3; ++a) {
+                    for (int i = 0; i < axes[a] / 2; i++) {
+                        const float angle = (float)pos[a] * f[a][i] / sf[a];
+                        row[off + 2 * i] = cosf(angle);
+                        row[off + 2 * i + 1] = sinf(angle);
+                    }
+                    off += axes[a];
+                }
+            }
+    return KD_FA_OK;
+}
+
+size_t kd_fa_rope_axes_size(int T, int Hp, int Wp, const int axes[3]) {
+    if (!axes_ok(T, Hp, Wp, axes)) return 0;
+    return (size_t)T * axes[0] + (size_t)Hp * axes[1] + (size_t)Wp * axes[2];
+}
+
+// The per-axis factors of compute_visual_rope: the t block of row
+// (t, h, w) equals axes-table row t of axis 0, and likewise for h and w.
+int kd_fa_rope_axes_fill(int T, int Hp, int Wp, const int axes[3], const float sf[3],
+                         float theta, float *out) {
+    if (!axes_ok(T, Hp, Wp, axes) || !sf || !out) return KD_FA_ERR_ROPE;
+    const int n[3] = {T, Hp, Wp};
+    float *dst = out;
+    for (int a = 0; a < 3; ++a) {
+        std::vector<float> f(axes[a] / 2 + 1);
+        rope_freqs(axes[a] / 2, theta, f.data());
+        for (int p = 0; p < n[a]; ++p) {
+            for (int i = 0; i < axes[a] / 2; ++i) {
+                const float angle = (float)p * f[i] / sf[a];
+                dst[2 * i] = cosf(angle);
+                dst[2 * i + 1] = sinf(angle);
+            }
+            dst += axes[a];
+        }
+    }
+    return KD_FA_OK;
+}
+
+// rope::compute_text_rope (src/rope.hpp:36-49).
+int kd_fa_rope_text_table(int L, int D, float theta, float *out) {
+    if (L < 0 || D <= 0 || D % 2 || !out) return KD_FA_ERR_ROPE;
+    std::vector<float> f(D / 2 + 1);
+    rope_freqs(D / 2, theta, f.data());
+    for (int pos = 0; pos < L; pos++)
+        for (int i = 0; i < D / 2; i++) {
+            const float angle = (float)pos * f[i];
+            out[(size_t)pos * D + 2 * i] = cosf(angle);
+            out[(size_t)pos * D + 2 * i + 1] = sinf(angle);
+        }
+    return KD_FA_OK;
+}
+
+const char *kd_fa_strerror(int status) {
+    switch (status) {
+    case KD_FA_OK: return "ok";
+    case KD_FA_ERR_NULL: return "null descriptor or data pointer";
+    case KD_FA_ERR_TYPE: return "unsupported tensor type";
+    case KD_FA_ERR_SHAPE: return "tensor shapes inconsistent with GGML_OP_FLASH_ATTN_EXT";
+    case KD_FA_ERR_LAYOUT: return "unsupported stride or alignment";
+    case KD_FA_ERR_PARAM: return "unsupported op parameter (max_bias, logit_softcap, scale)";
+    case KD_FA_ERR_ROPE: return "invalid RoPE descriptor";
+    case KD_FA_ERR_LAUNCH: return "HIP kernel launch failed";
+    case KD_FA_ERR_DEVICE: return "current device is not a gfx950 GPU";
+    default: return "unknown status";
+    }
+}
+
+int kd_fa_version(void) { return 100; }
+
+}  // extern "C"

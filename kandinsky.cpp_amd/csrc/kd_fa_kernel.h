@@ -1,0 +1,47 @@
+// kd_fa_kernel.h - launch arguments shared by the host glue (kd_fa_host.cpp)
+// and the gfx950 kernels (kd_fa_kernel.hip).  Internal to libkd_fa.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/kd_fa.h"
+
+namespace kdfa {
+
+// Byte strides are ggml's nb[1..3]; element strides nb[0] are the element
+// size (checked by kd_fa_supports).
+struct Args {
+    const char *q;
+    const char *k;
+    const char *v;
+    const char *m;      // F16 mask or nullptr
+    char *o;            // F32 dst [Dv, H, Lq, B]
+    int64_t q_nb1, q_nb2, q_nb3;
+    int64_t k_nb1, k_nb2, k_nb3;
+    int64_t v_nb1, v_nb2, v_nb3;
+    int64_t m_nb1, m_nb2, m_nb3;
+    int64_t o_nb1, o_nb2, o_nb3;
+    int32_t Lq, Lk, H, B;
+    int32_t rk2, rk3;   // H / Hk, B / Bk  (ggml broadcast ratios)
+    int32_t rv2, rv3;   // H / Hv, B / Bv
+    int32_t m_ne2, m_ne3;
+    int32_t q_type;     // KD_FA_TYPE_*
+    int32_t mask_vec;   // mask rows are 16-byte aligned
+    float scale_log2;   // scale * log2(e)
+    int32_t rope_mode;  // KD_FA_ROPE_*
+    const float *rope_tab;
+    int64_t rope_nb1;
+    const float *axes;
+    int32_t grid_t, grid_h, grid_w;
+    int32_t axis0, axis1, axis2;
+    int32_t n_qt;       // query tiles per (b, h)
+    int32_t n_blocks;   // n_qt * H * B
+};
+
+// Enqueue the forward kernel for K/V element type kv_type on `stream`.
+hipError_t launch(const Args &a, int kv_type, hipStream_t stream);
+
+constexpr int kBlockM = 128;
+
+}  // namespace kdfa

@@ -1,0 +1,174 @@
+"""The C ABI of libkd_fa.so, host side only (no GPU needed): the library
+loads, exports every function include/kd_fa.h declares, its structs have
+the layout ctypes assumes, and kd_fa_supports gives the answers that
+ggml_backend_supports_op would need (src/core/ops.hpp:179) -- accepting the
+node as the reference builds it and rejecting what the kernel cannot run,
+with the reason code, without touching a GPU."""
+import ctypes
+import os
+import subprocess
+import tempfile
+
+import pytest
+import torch
+
+import kd_fa
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_library_exports_every_header_symbol():
+    lib = kd_fa.lib()
+    syms = kd_fa.header_symbols()
+    assert len(syms) >= 10
+    for s in syms:
+        assert hasattr(lib, s), s
+    out = subprocess.run(["nm", "-D", "--defined-only", kd_fa.LIB_PATH], capture_output=True, text=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    assert set(syms) <= exported
+
+
+def test_struct_layout_matches_c():
+    src = r"""
+    #include <stdio.h>
+    #include <stddef.h>
+    #include "kd_fa.h"
+    int main(void) {
+      printf("%zu %zu %zu %zu %zu\n", sizeof(kd_fa_tensor), offsetof(kd_fa_tensor, ne),
+             offsetof(kd_fa_tensor, nb), offsetof(kd_fa_tensor, data), sizeof(kd_fa_desc));
+      printf("%zu %zu %zu %zu\n", offsetof(kd_fa_desc, dst), offsetof(kd_fa_desc, scale),
+             offsetof(kd_fa_desc, prec), sizeof(kd_fa_rope));
+      printf("%zu %zu %zu %zu\n", offsetof(kd_fa_rope, table), offsetof(kd_fa_rope, axes_data),
+             offsetof(kd_fa_rope, grid), offsetof(kd_fa_rope, axes));
+      return 0;
+    }
+    """
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "layout.c")
+        exe = os.path.join(d, "layout")
+        with open(c, "w") as f:
+            f.write(src)
+        subprocess.run(["gcc", "-std=c99", "-I", os.path.join(ROOT, "include"), c, "-o", exe], check=True)
+        got = [int(x) for x in subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split()]
+    T, Dd, R = kd_fa.KdFaTensor, kd_fa.KdFaDesc, kd_fa.KdFaRope
+    want = [ctypes.sizeof(T), T.ne.offset, T.nb.offset, T.data.offset, ctypes.sizeof(Dd),
+            Dd.dst.offset, Dd.scale.offset, Dd.prec.offset, ctypes.sizeof(R),
+            R.table.offset, R.axes_data.offset, R.grid.offset, R.axes.offset]
+    assert got == want
+
+
+def test_header_compiles_as_c_and_cxx():
+    for cc, std in (("gcc", "-std=c99"), ("g++", "-std=c++11")):
+        with tempfile.TemporaryDirectory() as d:
+            c = os.path.join(d, "t.c")
+            with open(c, "w") as f:
+                f.write('#include "kd_fa.h"\nint main(void){return kd_fa_version() < 0;}\n')
+            subprocess.run([cc, std, "-Wall", "-Werror", "-fsyntax-only", "-I", os.path.join(ROOT, "include"),
+                            "-x", "c" if cc == "gcc" else "c++", c], check=True)
+
+
+def test_version_and_strerror():
+    lib = kd_fa.lib()
+    assert lib.kd_fa_version() >= 100
+    for code in range(0, -9, -1):
+        assert lib.kd_fa_strerror(code)
+    assert b"unknown" in lib.kd_fa_strerror(-99)
+
+
+# ----------------------------------------------------------------------------
+# kd_fa_supports: the node as the reference builds it, and rejections
+# ----------------------------------------------------------------------------
+
+def _node(B=1, H=4, Lq=64, Lk=48, kt=torch.float16, qt=torch.float32, mask=False, Hkv=None):
+    """ops.hpp:122-177 as the reference calls it: q F32 [D, Lq, H], K/V F16."""
+    Hkv = H if Hkv is None else Hkv
+    q = torch.zeros((B, H, Lq, 128), dtype=qt)
+    k = torch.zeros((B, Hkv, Lk, 128), dtype=kt)
+    v = torch.zeros((B, Hkv, Lk, 128), dtype=kt)
+    m = torch.zeros((B, 1, Lq, Lk), dtype=torch.float16) if mask else None
+    dst = torch.zeros((B, Lq, H, 128), dtype=torch.float32)
+    return q, k, v, m, dst
+
+
+def _sup(q, k, v, m, dst, **kw):
+    return kd_fa.supports(q, k, v, m, dst, scale=kw.pop("scale", 0.08838834764831845), **kw)
+
+
+@pytest.mark.parametrize("qt,kt", [(torch.float32, torch.float16), (torch.bfloat16, torch.bfloat16),
+                                   (torch.float16, torch.float16), (torch.float32, torch.bfloat16)])
+def test_accepts_reference_node(qt, kt):
+    assert _sup(*_node(qt=qt, kt=kt)) == (True, 0)
+    assert _sup(*_node(qt=qt, kt=kt, mask=True, B=2)) == (True, 0)
+    assert _sup(*_node(qt=qt, kt=kt, H=8, Hkv=2)) == (True, 0)
+
+
+def test_rejections_carry_reason():
+    q, k, v, m, dst = _node()
+    assert _sup(q[..., :64], k[..., :64], v[..., :64], None, dst[..., :64]) == (False, kd_fa.ERR_SHAPE)
+    assert _sup(q, k, v, m, dst, max_bias=8.0) == (False, kd_fa.ERR_PARAM)
+    assert _sup(q, k, v, m, dst, logit_softcap=30.0) == (False, kd_fa.ERR_PARAM)
+    assert _sup(q, k, v, m, dst, scale=float("nan")) == (False, kd_fa.ERR_PARAM)
+    assert _sup(q, k.float(), v.float(), m, dst) == (False, kd_fa.ERR_TYPE)          # F32 K
+    assert _sup(q, k, v.to(torch.bfloat16), m, dst) == (False, kd_fa.ERR_TYPE)       # V type != K type
+    assert _sup(q, k, v, m, dst.half()) == (False, kd_fa.ERR_TYPE)                   # F16 dst
+    assert _sup(q, k, v, torch.zeros((1, 1, 64, 48)), dst) == (False, kd_fa.ERR_TYPE)  # F32 mask
+    assert _sup(q, k, v, torch.zeros((1, 1, 63, 48), dtype=torch.float16), dst) == (False, kd_fa.ERR_SHAPE)
+    assert _sup(q, k, v, torch.zeros((1, 1, 64, 47), dtype=torch.float16), dst) == (False, kd_fa.ERR_SHAPE)
+    assert _sup(*_node(H=6, Hkv=4)) == (False, kd_fa.ERR_SHAPE)                       # H % Hkv
+    assert _sup(q, k[:, :, :40], v, m, dst) == (False, kd_fa.ERR_SHAPE)               # Lk(K) != Lk(V)
+    assert _sup(q, k, v, m, dst[:, :, :2]) == (False, kd_fa.ERR_SHAPE)                # dst heads
+    # layouts: non-unit innermost stride, rows not 16-byte aligned
+    kk = torch.zeros((1, 4, 48, 136), dtype=torch.float16)[..., :128]                  # 272-byte rows
+    assert _sup(q, kk, v, m, dst) == (True, 0)
+    kk = torch.zeros((1, 4, 48, 132), dtype=torch.float16)[..., :128]                  # 264-byte rows
+    assert _sup(q, kk, v, m, dst) == (False, kd_fa.ERR_LAYOUT)
+    kt = torch.zeros((1, 4, 128, 48), dtype=torch.float16).transpose(-1, -2)           # ne0 stride != 2
+    assert _sup(q, kt, v, m, dst) == (False, kd_fa.ERR_LAYOUT)
+
+
+def test_null_and_empty():
+    lib = kd_fa.lib()
+    r = ctypes.c_int(0)
+    assert lib.kd_fa_supports(None, ctypes.byref(r)) == 0 and r.value == kd_fa.ERR_NULL
+    assert lib.kd_fa_run(None, None) == kd_fa.ERR_NULL
+    d = kd_fa.make_desc(*_node()[:3], None, _node()[4], 0.1)
+    d.k.data = None
+    assert lib.kd_fa_supports(ctypes.byref(d), ctypes.byref(r)) == 0 and r.value == kd_fa.ERR_NULL
+
+
+def test_rope_descriptor_checks():
+    q, k, v, m, dst = _node(Lq=60, Lk=60, qt=torch.bfloat16, kt=torch.bfloat16)
+    good = kd_fa.rope_table(torch.zeros((60, 128)))
+    assert _sup(q, k, v, None, dst, rope=good) == (True, 0)
+    assert _sup(q, k, v, None, dst, rope=kd_fa.rope_table(torch.zeros((59, 128)))) == (False, kd_fa.ERR_ROPE)
+    assert _sup(q, k, v, None, dst, rope=kd_fa.rope_table(torch.zeros((60, 64)))) == (False, kd_fa.ERR_ROPE)
+    assert _sup(q, k, v, None, dst, rope=kd_fa.rope_table(torch.zeros((60, 128), dtype=torch.float16))) \
+        == (False, kd_fa.ERR_ROPE)
+    buf = torch.zeros(1024)
+    assert _sup(q, k, v, None, dst, rope=kd_fa.rope_axes(buf, (3, 4, 5), (32, 48, 48))) == (True, 0)
+    assert _sup(q, k, v, None, dst, rope=kd_fa.rope_axes(buf, (3, 4, 4), (32, 48, 48))) == (False, kd_fa.ERR_ROPE)
+    assert _sup(q, k, v, None, dst, rope=kd_fa.rope_axes(buf, (3, 4, 5), (32, 48, 40))) == (False, kd_fa.ERR_ROPE)
+    assert _sup(q, k, v, None, dst, rope=kd_fa.rope_axes(buf, (3, 4, 5), (36, 44, 48))) == (False, kd_fa.ERR_ROPE)
+    bad = kd_fa.KdFaRope()
+    bad.mode = 7
+    assert _sup(q, k, v, None, dst, rope=bad) == (False, kd_fa.ERR_ROPE)
+    none = kd_fa.KdFaRope()
+    assert _sup(q, k, v, None, dst, rope=none) == (True, 0)
+
+
+def test_run_validates_before_touching_the_device():
+    """Invalid nodes return their error code from kd_fa_run with nothing
+    enqueued, on any host (the device is only queried for valid nodes)."""
+    q, k, v, m, dst = _node()
+    d = kd_fa.make_desc(q, k, v, m, dst, 0.1, max_bias=1.0)
+    assert kd_fa.lib().kd_fa_run(ctypes.byref(d), None) == kd_fa.ERR_PARAM
+    d = kd_fa.make_desc(q[..., :64], k[..., :64], v[..., :64], m, dst[..., :64], 0.1)
+    assert kd_fa.lib().kd_fa_run(ctypes.byref(d), None) == kd_fa.ERR_SHAPE
+
+
+def test_empty_query_is_a_no_op():
+    q, k, v, m, dst = _node(Lq=0)
+    d = kd_fa.make_desc(q, k, v, None, dst, 0.1)
+    d.q.data = 16        # zero rows: any aligned non-null pointer, never read
+    d.dst.data = 16
+    assert kd_fa.lib().kd_fa_run(ctypes.byref(d), None) == kd_fa.OK
