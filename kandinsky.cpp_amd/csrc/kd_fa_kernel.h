@@ -42,6 +42,6 @@ struct Args {
 // Enqueue the forward kernel for K/V element type kv_type on `stream`.
 hipError_t launch(const Args &a, int kv_type, hipStream_t stream);
 
-constexpr int kBlockM = 128;
+constexpr int kBlockM = 256;
 
 }  // namespace kdfa

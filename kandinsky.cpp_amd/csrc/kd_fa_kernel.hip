@@ -2,25 +2,32 @@
 // attention node (GGML_OP_FLASH_ATTN_EXT as src/core/ops.hpp:176 builds it),
 // with optional RoPE (src/rope.hpp:109-155) fused into the Q/K operand loads.
 //
-// One workgroup = 4 waves = 128 query rows of one (batch, head); each wave
-// owns 32 query rows for the whole key loop.  Per 64-key tile:
+// One workgroup = 8 waves = 256 query rows of one (batch, head); each wave
+// owns 32 query rows for the whole key loop, and two waves share each SIMD
+// so that one wave's softmax (VALU) overlaps the other's matrix products.
+// Per 64-key tile:
 //   S^T[key][query] = K Q^T   on v_mfma_f32_32x32x16_{bf16,f16}
-//   online softmax in F32 (exp2 domain, one cross-lane exchange per row)
+//   online softmax in F32 (exp2 domain, row max shared by a lane pair)
 //   O^T[d][query]  += V^T P^T on the same MFMA shape
-// K and V tiles are double-buffered in LDS (2 x 32 KiB), written through
-// registers so that RoPE (K) and the transpose (V) happen on the way in.
+// K and V tiles are double-buffered in LDS (2 x 32 KiB) and streamed
+// global -> LDS by the DMA path (global_load_lds, 16 bytes per lane) while
+// the previous tile is being computed.  With RoPE, K instead passes through
+// registers, where it is rotated on its way into LDS.
 //
 // Operand layouts of v_mfma_f32_32x32x16 (wave64):
 //   A (32 x 16): lane l holds row l%32, k = (l/32)*8 .. +7
 //   B (16 x 32): lane l holds column l%32, k = (l/32)*8 .. +7
 //   C (32 x 32): lane l, element i holds row 8*(i/4) + 4*(l/32) + i%4,
 //                column l%32
-// The S^T product uses A = K (keys on M) and B = Q^T (queries on N), so
-// each lane holds 16 scores of one query per 32-key block.  The K rows of
-// each 32-key block sit in LDS in "swapped" order (bits 2 and 3 of the key
-// index exchanged), which makes score element i of lane l belong to key
-// 16*(i/8) + 8*(l/32) + i%8: elements 0..7 and 8..15 are then exactly the
-// B operands (P^T, keys on K) of the two 16-key PV steps.
+// S^T uses A = K (keys on M) and B = Q^T (queries on N): each lane holds 16
+// scores of one query per 32-key block.  The K rows of each 32-key block sit
+// in LDS with bits 2 and 3 of the key index exchanged, which makes score
+// element i of lane l belong to key 16*(i/8) + 8*(l/32) + i%8: elements
+// 0..7 and 8..15 are then exactly the B operands (P^T) of the two 16-key PV
+// steps.  The PV A operand (V^T) is read from row-major V with
+// ds_read_b64_tr_b16: within each 16-lane group, source lane s supplies 4
+// elements and result lane j receives element j%4 of source lanes j/4 + 4r,
+// r = 0..3 -- one column of 4 consecutive keys per lane.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -36,15 +43,22 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kD = 128;        // head dim (Dk = Dv)
-constexpr int kBM = 128;       // query rows per workgroup
-constexpr int kBN = 64;        // keys per tile
-constexpr int kThreads = 256;  // 4 waves
-constexpr int kKBytes = kBN * kD * 2;   // one K tile in LDS
-constexpr int kVBytes = kD * kBN * 2;   // one V^T tile in LDS
-constexpr int kBufBytes = kKBytes + kVBytes;
+#define LDS_PTR(T, p) ((__attribute__((address_space(3))) T *)(p))
+
+constexpr int kD = 128;          // head dim (Dk = Dv)
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kBM = 32 * kWaves; // query rows per workgroup
+constexpr int kBN = 64;          // keys per tile
+constexpr int kTileBytes = kBN * kD * 2;   // one K or V tile
 constexpr float kLog2e = 1.4426950408889634f;
+// Lazy rescale: the running max moves only when a row max exceeds it by
+// more than kTau (log2 units), so P <= 2^kTau before normalisation.
+constexpr float kTau = 8.0f;
+
+static_assert(kBM == kBlockM, "block rows");
 
 // ---------------------------------------------------------------------
 // element-type traits: MFMA and F32 <-> storage conversions
@@ -73,12 +87,8 @@ template <> struct Elem<_Float16> {
         f16x2 v = __builtin_convertvector((f32x4){lo, hi, 0.f, 0.f}.xy, f16x2);
         return __builtin_bit_cast(uint32_t, v);
     }
-    static __device__ __forceinline__ float lo(uint32_t w) {
-        return (float)__builtin_bit_cast(f16x2, w).x;
-    }
-    static __device__ __forceinline__ float hi(uint32_t w) {
-        return (float)__builtin_bit_cast(f16x2, w).y;
-    }
+    static __device__ __forceinline__ float lo(uint32_t w) { return (float)__builtin_bit_cast(f16x2, w).x; }
+    static __device__ __forceinline__ float hi(uint32_t w) { return (float)__builtin_bit_cast(f16x2, w).y; }
 };
 
 static __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
@@ -86,9 +96,7 @@ static __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_f
 static __device__ __forceinline__ float f16_lo(uint32_t w) { return (float)__builtin_bit_cast(f16x2, w).x; }
 static __device__ __forceinline__ float f16_hi(uint32_t w) { return (float)__builtin_bit_cast(f16x2, w).y; }
 
-static __device__ __forceinline__ u32x4 ld16(const void *p) {
-    return *reinterpret_cast<const u32x4 *>(p);
-}
+static __device__ __forceinline__ u32x4 ld16(const void *p) { return *reinterpret_cast<const u32x4 *>(p); }
 
 // Eight consecutive elements of a row (16-byte aligned) as F32.
 static __device__ __forceinline__ void load8_f32(const char *p, int type, float x[8]) {
@@ -107,33 +115,24 @@ static __device__ __forceinline__ void load8_f32(const char *p, int type, float 
     }
 }
 
-// (cos, sin) pairs for columns d0 .. d0+7 of token `tok`.
-static __device__ __forceinline__ void rope_cs8(const Args &a, int tok, int d0, float cs[8]) {
-    const float *p;
-    if (a.rope_mode == KD_FA_ROPE_TABLE) {
-        p = reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.rope_tab) +
-                                            (int64_t)tok * a.rope_nb1) + d0;
-    } else {
-        const int hw = a.grid_h * a.grid_w;
-        if (d0 < a.axis0) {
-            p = a.axes + (tok / hw) * a.axis0 + d0;
-        } else if (d0 < a.axis0 + a.axis1) {
-            p = a.axes + a.grid_t * a.axis0 + ((tok / a.grid_w) % a.grid_h) * a.axis1 + (d0 - a.axis0);
-        } else {
-            p = a.axes + a.grid_t * a.axis0 + a.grid_h * a.axis1 + (tok % a.grid_w) * a.axis2 +
-                (d0 - a.axis0 - a.axis1);
-        }
-    }
-    const f32x4 u = *reinterpret_cast<const f32x4 *>(p);
-    const f32x4 v = *reinterpret_cast<const f32x4 *>(p + 4);
-    cs[0] = u.x; cs[1] = u.y; cs[2] = u.z; cs[3] = u.w;
-    cs[4] = v.x; cs[5] = v.y; cs[6] = v.z; cs[7] = v.w;
+// Address of the (cos, sin) pairs for columns d0 .. d0+7 of token `tok`.
+static __device__ __forceinline__ const float *rope_ptr(const Args &a, int tok, int d0) {
+    if (a.rope_mode == KD_FA_ROPE_TABLE)
+        return reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.rope_tab) +
+                                               (int64_t)tok * a.rope_nb1) + d0;
+    const int hw = a.grid_h * a.grid_w;
+    if (d0 < a.axis0) return a.axes + (tok / hw) * a.axis0 + d0;
+    if (d0 < a.axis0 + a.axis1)
+        return a.axes + a.grid_t * a.axis0 + ((tok / a.grid_w) % a.grid_h) * a.axis1 + (d0 - a.axis0);
+    return a.axes + a.grid_t * a.axis0 + a.grid_h * a.axis1 + (tok % a.grid_w) * a.axis2 +
+           (d0 - a.axis0 - a.axis1);
 }
 
 // rope::apply's pair rotation (src/rope.hpp:137-138): every product and
 // every sum rounded to F32 on its own, as the separate ggml ops do.
-static __device__ __forceinline__ void rotate8(float x[8], const float cs[8]) {
+static __device__ __forceinline__ void rotate8(float x[8], f32x4 c0, f32x4 c1) {
 #pragma clang fp contract(off)
+    const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
     for (int j = 0; j < 4; ++j) {
         const float x0 = x[2 * j], x1 = x[2 * j + 1];
         const float c = cs[2 * j], s = cs[2 * j + 1];
@@ -143,23 +142,43 @@ static __device__ __forceinline__ void rotate8(float x[8], const float cs[8]) {
     }
 }
 
-// Key index inside a 64-key tile <-> LDS row of the K tile (bits 2 and 3
-// exchanged; the map is its own inverse).
+// K tile: LDS row r holds key k_row_of(r) (bits 2 and 3 exchanged, its own
+// inverse); 16-byte chunk c of a row is stored at c ^ (r & 15).
+// V tile: row r holds key r; chunk c is stored at c ^ v_swz(r).  Both keep
+// the MFMA operand reads free of bank conflicts on 32- and 64-bank LDS.
 static __device__ __forceinline__ int k_row_of(int key) {
     return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
 }
+static __device__ __forceinline__ int v_swz(int r) { return ((r & 3) << 2) | (r & 2); }
 
-// XOR swizzles of the 16-byte chunks of a K row (16 chunks) and of a V^T
-// row (8 chunks): every group of 16 (or 8) lanes that reads one logical
-// chunk column hits distinct banks.
-static __device__ __forceinline__ int k_chunk(int row, int c) { return c ^ (row & 15); }
-static __device__ __forceinline__ int v_chunk(int d, int c) { return c ^ ((d & 7) ^ ((d >> 3) & 1)); }
+static __device__ __forceinline__ void dma16(const void *g, char *lds_wave_base) {
+    __builtin_amdgcn_global_load_lds(g, LDS_PTR(void, lds_wave_base), 16, 0, 0);
+}
+
+static __device__ __forceinline__ float max3(float a, float b, float c) {
+    return __builtin_fmaxf(a, __builtin_fmaxf(b, c));
+}
+
+// max over the lane pair (l, l ^ 32) that shares one query row
+static __device__ __forceinline__ float pair_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+static __device__ __forceinline__ float pair_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 template <typename T, bool HAS_MASK, bool ROPE>
 __global__ __launch_bounds__(kThreads) void fa_fwd_d128(Args a) {
     typedef Elem<T> E;
     typedef typename E::vec8 vec8;
-    __shared__ __attribute__((aligned(16))) char smem[2 * kBufBytes];
+    // four distinct LDS objects (not one array) so that the compiler can
+    // tell the tile being computed from the tile the DMA is filling
+    __shared__ __attribute__((aligned(1024))) char sK0[kTileBytes];
+    __shared__ __attribute__((aligned(1024))) char sK1[kTileBytes];
+    __shared__ __attribute__((aligned(1024))) char sV0[kTileBytes];
+    __shared__ __attribute__((aligned(1024))) char sV1[kTileBytes];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -180,8 +199,9 @@ __global__ __launch_bounds__(kThreads) void fa_fwd_d128(Args a) {
 
     const char *kbase = a.k + (int64_t)(h / a.rk2) * a.k_nb2 + (int64_t)(b / a.rk3) * a.k_nb3;
     const char *vbase = a.v + (int64_t)(h / a.rv2) * a.v_nb2 + (int64_t)(b / a.rv3) * a.v_nb3;
+    const int Lk = a.Lk;
 
-    // ---- Q fragment (B operand of S^T): row q_row, k-steps of 16 -------
+    // ---- Q fragment (B operand of S^T): row q_row, k-steps of 16 -----------
     const int q_row = qt * kBM + wave * 32 + l32;
     const int q_ld = q_row < a.Lq ? q_row : a.Lq - 1;
     vec8 qf[8];
@@ -194,12 +214,14 @@ __global__ __launch_bounds__(kThreads) void fa_fwd_d128(Args a) {
             float x[8];
             load8_f32(qp + d0 * esz, a.q_type, x);
             if (ROPE) {
-                float cs[8];
-                rope_cs8(a, q_ld, d0, cs);
-                rotate8(x, cs);
+                const float *cp = rope_ptr(a, q_ld, d0);
+                rotate8(x, *reinterpret_cast<const f32x4 *>(cp), *reinterpret_cast<const f32x4 *>(cp + 4));
             }
             u32x4 w;
             for (int j = 0; j < 4; ++j) w[j] = E::pack2(x[2 * j], x[2 * j + 1]);
+            // scale < 0: use -q (exact) and |scale|, so that every score
+            // below is s * c2 with c2 >= 0 and its max is max(s) * c2
+            if (a.scale_log2 < 0.0f) w ^= (u32x4){0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
             qf[ks] = __builtin_bit_cast(vec8, w);
         }
     }
@@ -214,192 +236,255 @@ __global__ __launch_bounds__(kThreads) void fa_fwd_d128(Args a) {
     f32x16 o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = (f32x16){};
-    float m_run = -INFINITY;
-    float l_run = 0.0f;
+    float m_run = -INFINITY;   // running max (log2 units), same in both lanes of a pair
+    float l_half = 0.0f;       // running sum over this lane's half of the keys
 
-    // ---- tile staging: global -> registers -> (RoPE / transpose) -> LDS --
-    // K: thread handles chunks u = tid + 256*j: key u/16, 16-byte chunk u%16.
-    // V: thread handles keys 4*(tid%16) .. +3 at d-chunk tid/16.
-    const int v_kq = tid & 15;
-    const int v_dc = tid >> 4;
-    u32x4 kr[4], vr[4];
-
-    auto load_tile = [&](int t) {
+    // ---- tile staging -------------------------------------------------------
+    // DMA: each wave fills 1 KiB (4 rows) of a tile per instruction; wave w
+    // covers rows 4*(w + 8j) .. +3, j = 0, 1, for K and for V.
+    const int dma_row = lane >> 4;        // row within the wave's 4 rows
+    const int dma_pc = lane & 15;         // physical chunk this lane fills
+    auto issue_tile = [&](int t, char *dK, char *dV) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int u = tid + kThreads * j;
-            const int gk = t * kBN + (u >> 4);
-            kr[j] = gk < a.Lk ? ld16(kbase + (int64_t)gk * a.k_nb1 + (u & 15) * 16) : (u32x4){0, 0, 0, 0};
+        for (int j = 0; j < 2; ++j) {
+            const int r = 4 * (wave + 8 * j) + dma_row;
+            int gk = t * kBN + r;
+            gk = gk < Lk ? gk : Lk - 1;
+            dma16(vbase + (int64_t)gk * a.v_nb1 + ((dma_pc ^ v_swz(r)) << 4),
+                  dV + (wave + 8 * j) * 1024);
         }
+        if (!ROPE) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int gk = t * kBN + 4 * v_kq + j;
-            vr[j] = gk < a.Lk ? ld16(vbase + (int64_t)gk * a.v_nb1 + v_dc * 16) : (u32x4){0, 0, 0, 0};
-        }
-    };
-
-    auto store_tile = [&](int t, int buf) {
-        char *ks_ = smem + buf * kBufBytes;
-        char *vt_ = ks_ + kKBytes;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int u = tid + kThreads * j;
-            const int key = u >> 4, c = u & 15;
-            u32x4 w = kr[j];
-            if (ROPE) {
-                const int gk = t * kBN + key;
-                if (gk < a.Lk) {
-                    float x[8], cs[8];
-                    for (int e = 0; e < 4; ++e) { x[2 * e] = E::lo(w[e]); x[2 * e + 1] = E::hi(w[e]); }
-                    rope_cs8(a, gk, c * 8, cs);
-                    rotate8(x, cs);
-                    for (int e = 0; e < 4; ++e) w[e] = E::pack2(x[2 * e], x[2 * e + 1]);
-                }
+            for (int j = 0; j < 2; ++j) {
+                const int r = 4 * (wave + 8 * j) + dma_row;
+                int gk = t * kBN + k_row_of(r);
+                gk = gk < Lk ? gk : Lk - 1;
+                dma16(kbase + (int64_t)gk * a.k_nb1 + ((dma_pc ^ (r & 15)) << 4),
+                      dK + (wave + 8 * j) * 1024);
             }
-            const int row = k_row_of(key);
-            *reinterpret_cast<u32x4 *>(ks_ + row * 256 + k_chunk(row, c) * 16) = w;
         }
-        // V^T: for d = 8*v_dc + e, keys 4*v_kq .. +3 -> 8 bytes
+    };
+    // RoPE: K chunk u = tid + 512*j -> LDS row u/16, physical chunk u%16.
+    u32x4 kreg[2];
+    f32x4 kcs[2][2];
+    auto rope_load = [&](int t) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int d = v_dc * 8 + e;
-            const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-            const uint32_t w0 = __builtin_amdgcn_perm(vr[1][e >> 1], vr[0][e >> 1], sel);
-            const uint32_t w1 = __builtin_amdgcn_perm(vr[3][e >> 1], vr[2][e >> 1], sel);
-            const int c = v_kq >> 1;
-            *reinterpret_cast<u32x2 *>(vt_ + d * 128 + v_chunk(d, c) * 16 + (v_kq & 1) * 8) = (u32x2){w0, w1};
+        for (int j = 0; j < 2; ++j) {
+            const int u = tid + kThreads * j;
+            const int r = u >> 4;
+            const int c = (u & 15) ^ (r & 15);
+            int gk = t * kBN + k_row_of(r);
+            gk = gk < Lk ? gk : Lk - 1;
+            kreg[j] = ld16(kbase + (int64_t)gk * a.k_nb1 + c * 16);
+            const float *cp = rope_ptr(a, gk, c * 8);
+            kcs[j][0] = *reinterpret_cast<const f32x4 *>(cp);
+            kcs[j][1] = *reinterpret_cast<const f32x4 *>(cp + 4);
+        }
+    };
+    auto rope_store = [&](char *dK) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int u = tid + kThreads * j;
+            float x[8];
+            for (int e = 0; e < 4; ++e) { x[2 * e] = E::lo(kreg[j][e]); x[2 * e + 1] = E::hi(kreg[j][e]); }
+            rotate8(x, kcs[j][0], kcs[j][1]);
+            u32x4 w;
+            for (int e = 0; e < 4; ++e) w[e] = E::pack2(x[2 * e], x[2 * e + 1]);
+            *reinterpret_cast<u32x4 *>(dK + u * 16) = w;
         }
     };
 
-    const int n_tiles = (a.Lk + kBN - 1) / kBN;
+    // mask values of this lane's 32 keys (key 16*hh + 8*hi + e of 32-key
+    // block mb at index mb*16 + hh*8 + e), prefetched one tile ahead
+    u32x4 mraw[4];
+    auto mask_load = [&](int t) {
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int k0 = t * kBN + mb * 32 + hh * 16 + hi * 8;
+                u32x4 w;
+                if (a.mask_vec && k0 + 8 <= Lk) {
+                    w = ld16(mrow + k0);
+                } else {
+                    uint16_t e16[8];
+                    for (int e = 0; e < 8; ++e) e16[e] = k0 + e < Lk ? mrow[k0 + e] : (uint16_t)0xfc00u;
+                    for (int e = 0; e < 4; ++e) w[e] = (uint32_t)e16[2 * e] | ((uint32_t)e16[2 * e + 1] << 16);
+                }
+                mraw[mb * 2 + hh] = w;
+            }
+    };
+
+    const int n_tiles = (Lk + kBN - 1) / kBN;
     if (n_tiles > 0) {
-        load_tile(0);
-        store_tile(0, 0);
+        issue_tile(0, sK0, sV0);
+        if (ROPE) {
+            rope_load(0);
+            rope_store(sK0);
+        }
+        if (HAS_MASK) mask_load(0);
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 
-    const float c2 = a.scale_log2;
-    for (int t = 0; t < n_tiles; ++t) {
-        const int buf = t & 1;
+    const float c2 = __builtin_fabsf(a.scale_log2);
+    // K-operand LDS offset of this lane (rows l32 and 32 + l32 share the swizzle)
+    const int k_off = l32 * 256;
+    const int k_swz = lane & 15;
+    // V-operand (ds_read_b64_tr_b16) LDS offsets of this lane
+    const int v_sub = (lane & 15) >> 2;            // row within a 4-row group
+    const int v_g1 = (lane >> 4) & 1;
+    const int v_c_lo = 2 * v_g1 + ((lane & 3) >> 1);
+    const int v_byte = 8 * (lane & 1);
+
+    auto step = [&](int t, const char *ks_, const char *vs_, char *nK, char *nV) {
         const bool has_next = t + 1 < n_tiles;
-        if (has_next) load_tile(t + 1);
+        if (has_next) {
+            issue_tile(t + 1, nK, nV);
+            if (ROPE) rope_load(t + 1);
+        }
 
-        const char *ks_ = smem + buf * kBufBytes;
-        const char *vt_ = ks_ + kKBytes;
-
-        // mask values of this lane's 32 keys (keys 16*hh + 8*hi + e of each
-        // 32-key block mb), as F32; -inf also marks keys >= Lk
         float mv[32];
         bool live = true;
         if (HAS_MASK) {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    mv[q4 * 8 + 2 * e] = f16_lo(mraw[q4][e]);
+                    mv[q4 * 8 + 2 * e + 1] = f16_hi(mraw[q4][e]);
+                }
             bool any = false;
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const int k0 = t * kBN + mb * 32 + hh * 16 + hi * 8;
-                    float x[8];
-                    if (a.mask_vec && k0 + 8 <= a.Lk) {
-                        const u32x4 w = ld16(mrow + k0);
-                        for (int j = 0; j < 4; ++j) { x[2 * j] = f16_lo(w[j]); x[2 * j + 1] = f16_hi(w[j]); }
-                    } else {
-                        for (int e = 0; e < 8; ++e) {
-                            if (k0 + e < a.Lk) {
-                                const uint16_t hb = mrow[k0 + e];
-                                x[e] = (float)__builtin_bit_cast(_Float16, hb);
-                            } else {
-                                x[e] = -INFINITY;
-                            }
-                        }
-                    }
-                    for (int e = 0; e < 8; ++e) {
-                        mv[mb * 16 + hh * 8 + e] = x[e];
-                        any |= x[e] != -INFINITY;
-                    }
-                }
+            for (int i = 0; i < 32; ++i) any |= mv[i] != -INFINITY;
             live = __builtin_amdgcn_ballot_w64(any) != 0;
+            if (has_next) mask_load(t + 1);
         }
 
         if (live) {
             // ---- S^T = K Q^T ------------------------------------------------
-            f32x16 s[2];
+            f32x16 s0 = (f32x16){}, s1 = (f32x16){};
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb) {
-                s[mb] = (f32x16){};
-                const int row = mb * 32 + l32;
-#pragma unroll
-                for (int ks = 0; ks < 8; ++ks) {
-                    const int c = ks * 2 + hi;
-                    const vec8 ka = *reinterpret_cast<const vec8 *>(ks_ + row * 256 + k_chunk(row, c) * 16);
-                    s[mb] = E::mfma(ka, qf[ks], s[mb]);
-                }
+            for (int ks = 0; ks < 8; ++ks) {
+                const int off = k_off + (((2 * ks + hi) ^ k_swz) << 4);
+                const vec8 a0 = *reinterpret_cast<const vec8 *>(ks_ + off);
+                const vec8 a1 = *reinterpret_cast<const vec8 *>(ks_ + off + 32 * 256);
+                s0 = E::mfma(a0, qf[ks], s0);
+                s1 = E::mfma(a1, qf[ks], s1);
             }
 
             // ---- online softmax (log2 domain) -------------------------------
-            float x[32];
-            const bool tail = (t + 1) * kBN > a.Lk;
+            float p[32];
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
+            for (int i = 0; i < 16; ++i) {
+                p[i] = s0[i];
+                p[16 + i] = s1[i];
+            }
+            if (!HAS_MASK) {
+                // keys past Lk (last tile only): -inf raw scores for the max
+                // (each lane pair still holds the tile's first key, which is
+                // valid) and -inf exponents below
+                const bool tail = (t + 1) * kBN > Lk;
+                if (tail) {
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    float v = s[mb][i] * c2;
-                    if (HAS_MASK) {
-                        const float m = mv[mb * 16 + i];
-                        v = m == -INFINITY ? -INFINITY : __builtin_fmaf(m, kLog2e, v);
+                    for (int i = 0; i < 32; ++i) {
+                        const int key = t * kBN + (i >> 4) * 32 + 16 * ((i >> 3) & 1) + 8 * hi + (i & 7);
+                        p[i] = key < Lk ? p[i] : -INFINITY;
                     }
-                    if (tail) {
-                        const int key = t * kBN + mb * 32 + 16 * (i >> 3) + 8 * hi + (i & 7);
-                        if (key >= a.Lk) v = -INFINITY;
-                    }
-                    x[mb * 16 + i] = v;
                 }
-            float mx = x[0];
+                float mx = max3(p[0], p[1], p[2]);
 #pragma unroll
-            for (int i = 1; i < 32; ++i) mx = fmaxf(mx, x[i]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float m_new = fmaxf(m_run, mx);
-            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+                for (int i = 3; i < 31; i += 2) mx = max3(mx, p[i], p[i + 1]);
+                mx = __builtin_fmaxf(mx, p[31]);
+                mx = pair_max(mx) * c2;
+                if (__builtin_amdgcn_ballot_w64(mx > m_run + kTau) != 0) {
+                    const float m_new = __builtin_fmaxf(m_run, mx);
+                    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+                    m_run = m_new;
+                    l_half *= alpha;
+#pragma unroll
+                    for (int dblk = 0; dblk < 4; ++dblk)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) o[dblk][i] *= alpha;
+                }
+                const float nm = -m_run;
+#pragma unroll
+                for (int i = 0; i < 32; ++i) p[i] = __builtin_fmaf(p[i], c2, nm);
+                if (tail) {
+#pragma unroll
+                    for (int i = 0; i < 32; ++i) {
+                        const int key = t * kBN + (i >> 4) * 32 + 16 * ((i >> 3) & 1) + 8 * hi + (i & 7);
+                        p[i] = key < Lk ? p[i] : -INFINITY;
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 32; ++i) p[i] = __builtin_amdgcn_exp2f(p[i]);
+            } else {
+                // log2-domain logits s*c2 + mask*log2(e); -inf mask entries
+                // (and keys past Lk, filled with -inf) stay -inf
+#pragma unroll
+                for (int i = 0; i < 32; ++i)
+                    p[i] = mv[i] == -INFINITY ? -INFINITY : __builtin_fmaf(mv[i], kLog2e, p[i] * c2);
+                float mx = max3(p[0], p[1], p[2]);
+#pragma unroll
+                for (int i = 3; i < 31; i += 2) mx = max3(mx, p[i], p[i + 1]);
+                mx = __builtin_fmaxf(mx, p[31]);
+                mx = pair_max(mx);
+                if (__builtin_amdgcn_ballot_w64(mx > m_run + kTau) != 0) {
+                    const float m_new = __builtin_fmaxf(m_run, mx);
+                    const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+                    m_run = m_new;
+                    l_half *= alpha;
+#pragma unroll
+                    for (int dblk = 0; dblk < 4; ++dblk)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) o[dblk][i] *= alpha;
+                }
+                const float mu = m_run == -INFINITY ? 0.0f : m_run;
+#pragma unroll
+                for (int i = 0; i < 32; ++i) p[i] = __builtin_amdgcn_exp2f(p[i] - mu);
+            }
             float sum = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 32; ++i) {
-                x[i] = __builtin_amdgcn_exp2f(x[i] - m_use);
-                sum += x[i];
-            }
-            sum += __shfl_xor(sum, 32);
-            l_run = l_run * alpha + sum;
-            m_run = m_new;
-            if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
-#pragma unroll
-                for (int dblk = 0; dblk < 4; ++dblk)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) o[dblk][i] *= alpha;
-            }
+            for (int i = 0; i < 32; ++i) sum += p[i];
+            l_half += sum;
 
             // ---- O^T += V^T P^T ----------------------------------------------
+            vec8 pb[4];
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
+            for (int kst = 0; kst < 4; ++kst) {
+                u32x4 w;
+                for (int j = 0; j < 4; ++j) w[j] = E::pack2(p[8 * kst + 2 * j], p[8 * kst + 2 * j + 1]);
+                pb[kst] = __builtin_bit_cast(vec8, w);
+            }
 #pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    u32x4 pw;
-                    const int base = mb * 16 + kk * 8;
-                    for (int j = 0; j < 4; ++j) pw[j] = E::pack2(x[base + 2 * j], x[base + 2 * j + 1]);
-                    const vec8 pb = __builtin_bit_cast(vec8, pw);
-                    const int c = mb * 4 + kk * 2 + hi;
+            for (int kst = 0; kst < 4; ++kst) {
 #pragma unroll
-                    for (int dblk = 0; dblk < 4; ++dblk) {
-                        const int d = dblk * 32 + l32;
-                        const vec8 va = *reinterpret_cast<const vec8 *>(vt_ + d * 128 + v_chunk(d, c) * 16);
-                        o[dblk] = E::mfma(va, pb, o[dblk]);
-                    }
+                for (int dblk = 0; dblk < 4; ++dblk) {
+                    const int c = 4 * dblk + v_c_lo;
+                    const int r0 = 16 * kst + 8 * hi + v_sub;
+                    const int r1 = r0 + 4;
+                    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        LDS_PTR(s16x4, vs_ + r0 * 256 + ((c ^ v_swz(r0)) << 4) + v_byte));
+                    const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        LDS_PTR(s16x4, vs_ + r1 * 256 + ((c ^ v_swz(r1)) << 4) + v_byte));
+                    const vec8 va = __builtin_bit_cast(vec8, __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+                    o[dblk] = E::mfma(va, pb[kst], o[dblk]);
                 }
+            }
         }
 
-        if (has_next) store_tile(t + 1, buf ^ 1);
+        if (ROPE && has_next) rope_store(nK);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+    };
+    for (int t = 0; t < n_tiles; t += 2) {
+        step(t, sK0, sV0, sK1, sV1);
+        if (t + 1 < n_tiles) step(t + 1, sK1, sV1, sK0, sV0);
     }
 
     // ---- epilogue: O / l -> dst[b][q][h][:] (F32) ---------------------------
+    const float l_run = pair_sum(l_half);
     if (q_row < a.Lq) {
         const float inv = l_run == 0.0f ? 0.0f : 1.0f / l_run;
         char *op = a.o + (int64_t)b * a.o_nb3 + (int64_t)q_row * a.o_nb2 + (int64_t)h * a.o_nb1;

@@ -127,6 +127,18 @@ def test_strided_activation_views():
     assert_parity(gather_rows(out, np.arange(H * L), H, L), ref, "strided")
 
 
+@pytest.mark.parametrize("scale", [-0.0883883, 0.0, 0.5], ids=["neg", "zero", "large"])
+def test_scale_values(scale):
+    """Any finite scale: a negative one is applied as |scale| on -q."""
+    _need_gpu()
+    _announce(f"scale {scale}")
+    q, k, v = qkv(1, 2, 70, 90, torch.bfloat16, seed=17)
+    qg, kg, vg = _gpu(q, k, v)
+    out = _run(qg, kg, vg, scale=scale)
+    ref = orc.fa_f64(q, k, v, scale=scale)
+    assert_parity(gather_rows(out, np.arange(2 * 70), 2, 70), ref, f"scale {scale}")
+
+
 def test_deterministic():
     _need_gpu()
     _announce("determinism")
