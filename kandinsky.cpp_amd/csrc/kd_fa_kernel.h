@@ -42,6 +42,10 @@ struct Args {
 // Enqueue the forward kernel for K/V element type kv_type on `stream`.
 hipError_t launch(const Args &a, int kv_type, hipStream_t stream);
 
-constexpr int kBlockM = 256;
+// Waves per workgroup (32 query rows each).
+#ifndef KD_FA_WAVES
+#define KD_FA_WAVES 8
+#endif
+constexpr int kBlockM = 32 * KD_FA_WAVES;
 
 }  // namespace kdfa

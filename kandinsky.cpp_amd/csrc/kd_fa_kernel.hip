@@ -46,19 +46,37 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 #define LDS_PTR(T, p) ((__attribute__((address_space(3))) T *)(p))
+// LDS addresses are handled as 32-bit address-space-3 pointers throughout
+// (generic pointers would cost two registers each)
+typedef __attribute__((address_space(3))) char lds_t;
 
 constexpr int kD = 128;          // head dim (Dk = Dv)
-constexpr int kWaves = 8;
+constexpr int kWaves = KD_FA_WAVES;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBM = 32 * kWaves; // query rows per workgroup
 constexpr int kBN = 64;          // keys per tile
 constexpr int kTileBytes = kBN * kD * 2;   // one K or V tile
+constexpr int kRounds = kTileBytes / (kThreads * 16);  // 16-byte loads per thread per tile
 constexpr float kLog2e = 1.4426950408889634f;
 // Lazy rescale: the running max moves only when a row max exceeds it by
 // more than kTau (log2 units), so P <= 2^kTau before normalisation.
 constexpr float kTau = 8.0f;
+// Unmasked path: a row's weights against the running max may grow up to
+// this sum before the max is refreshed (2^64: no F32 overflow of O for any
+// |V| < 2^40 and Lk < 2^20).
+constexpr float kSumCap = 18446744073709551616.0f;
 
 static_assert(kBM == kBlockM, "block rows");
+
+// Wave priority around the MFMA sections (tuning switch).
+#ifndef KD_FA_SETPRIO
+#define KD_FA_SETPRIO 0
+#endif
+#if KD_FA_SETPRIO
+#define KD_FA_PRIO(x) __builtin_amdgcn_s_setprio(x)
+#else
+#define KD_FA_PRIO(x) ((void)0)
+#endif
 
 // ---------------------------------------------------------------------
 // element-type traits: MFMA and F32 <-> storage conversions
@@ -76,6 +94,11 @@ template <> struct Elem<__bf16> {
     }
     static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
     static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+    // acc + lo(w) + hi(w), exact products by 1.0 (v_dot2c_f32_bf16)
+    static __device__ __forceinline__ float sum2(uint32_t w, float acc) {
+        const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one, acc, false);
+    }
 };
 
 template <> struct Elem<_Float16> {
@@ -89,6 +112,10 @@ template <> struct Elem<_Float16> {
     }
     static __device__ __forceinline__ float lo(uint32_t w) { return (float)__builtin_bit_cast(f16x2, w).x; }
     static __device__ __forceinline__ float hi(uint32_t w) { return (float)__builtin_bit_cast(f16x2, w).y; }
+    static __device__ __forceinline__ float sum2(uint32_t w, float acc) {
+        const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, acc, false);
+    }
 };
 
 static __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
@@ -151,12 +178,35 @@ static __device__ __forceinline__ int k_row_of(int key) {
 }
 static __device__ __forceinline__ int v_swz(int r) { return ((r & 3) << 2) | (r & 2); }
 
-static __device__ __forceinline__ void dma16(const void *g, char *lds_wave_base) {
-    __builtin_amdgcn_global_load_lds(g, LDS_PTR(void, lds_wave_base), 16, 0, 0);
+// One wave-wide 16-byte-per-lane DMA: global (base + lane offset) -> LDS
+// (wave-uniform destination + 16 * lane).  Written as the instruction itself
+// so that the uniform base stays in SGPRs with a 32-bit lane offset (no
+// per-lane 64-bit address registers); the compiler does not track it, so
+// every consumer waits with an explicit s_waitcnt vmcnt(0) + barrier.
+static __device__ __forceinline__ void dma16(const char *base, uint32_t lane_off, lds_t *lds_wave_base) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_wave_base);
+    asm volatile("global_load_lds_dwordx4 %0, %1" :: "v"(lane_off), "s"(base), "{m0}"(m0));
 }
 
+// v_max3_f32 directly: the maxnum builtins would first canonicalise every
+// input (one extra v_max_f32 each) to quiet signalling NaNs, which the
+// scores never are
 static __device__ __forceinline__ float max3(float a, float b, float c) {
-    return __builtin_fmaxf(a, __builtin_fmaxf(b, c));
+    float d;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+
+// max of 32 values: two interleaved chains of v_max3_f32
+static __device__ __forceinline__ float max32(const float *p) {
+    float x = max3(p[0], p[1], p[2]);
+    float y = max3(p[3], p[4], p[5]);
+#pragma unroll
+    for (int i = 6; i < 30; i += 4) {
+        x = max3(x, p[i], p[i + 1]);
+        y = max3(y, p[i + 2], p[i + 3]);
+    }
+    return max3(x, y, __builtin_fmaxf(p[30], p[31]));
 }
 
 // max over the lane pair (l, l ^ 32) that shares one query row
@@ -170,19 +220,22 @@ static __device__ __forceinline__ float pair_sum(float x) {
 }
 
 template <typename T, bool HAS_MASK, bool ROPE>
-__global__ __launch_bounds__(kThreads) void fa_fwd_d128(Args a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void fa_fwd_d128(Args a) {
     typedef Elem<T> E;
     typedef typename E::vec8 vec8;
     // four distinct LDS objects (not one array) so that the compiler can
     // tell the tile being computed from the tile the DMA is filling
-    __shared__ __attribute__((aligned(1024))) char sK0[kTileBytes];
-    __shared__ __attribute__((aligned(1024))) char sK1[kTileBytes];
-    __shared__ __attribute__((aligned(1024))) char sV0[kTileBytes];
-    __shared__ __attribute__((aligned(1024))) char sV1[kTileBytes];
+    __shared__ __attribute__((aligned(1024))) char lK0[kTileBytes];
+    __shared__ __attribute__((aligned(1024))) char lK1[kTileBytes];
+    __shared__ __attribute__((aligned(1024))) char lV0[kTileBytes];
+    __shared__ __attribute__((aligned(1024))) char lV1[kTileBytes];
+    lds_t *const sK0 = LDS_PTR(char, lK0), *const sK1 = LDS_PTR(char, lK1);
+    lds_t *const sV0 = LDS_PTR(char, lV0), *const sV1 = LDS_PTR(char, lV1);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: SGPR
     const int l32 = lane & 31;
     const int hi = lane >> 5;
 
@@ -241,35 +294,58 @@ __global__ __launch_bounds__(kThreads) void fa_fwd_d128(Args a) {
 
     // ---- tile staging -------------------------------------------------------
     // DMA: each wave fills 1 KiB (4 rows) of a tile per instruction; wave w
-    // covers rows 4*(w + 8j) .. +3, j = 0, 1, for K and for V.
+    // covers rows 4*(w + kWaves*j) .. +3, j < kRounds, for K and for V.  The source
+    // is a uniform tile base plus a fixed per-lane offset; only a partial
+    // last tile clamps its rows to Lk - 1.
     const int dma_row = lane >> 4;        // row within the wave's 4 rows
     const int dma_pc = lane & 15;         // physical chunk this lane fills
-    auto issue_tile = [&](int t, char *dK, char *dV) {
+    uint32_t k_dma[kRounds], v_dma[kRounds];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int r = 4 * (wave + 8 * j) + dma_row;
-            int gk = t * kBN + r;
-            gk = gk < Lk ? gk : Lk - 1;
-            dma16(vbase + (int64_t)gk * a.v_nb1 + ((dma_pc ^ v_swz(r)) << 4),
-                  dV + (wave + 8 * j) * 1024);
-        }
-        if (!ROPE) {
+    for (int j = 0; j < kRounds; ++j) {
+        const int r = 4 * (wave + kWaves * j) + dma_row;
+        v_dma[j] = (uint32_t)r * (uint32_t)a.v_nb1 + ((dma_pc ^ v_swz(r)) << 4);
+        k_dma[j] = (uint32_t)k_row_of(r) * (uint32_t)a.k_nb1 + ((dma_pc ^ (r & 15)) << 4);
+    }
+    auto issue_v = [&](int t, lds_t *dV) {
+        const char *vt = vbase + (int64_t)t * kBN * a.v_nb1;
+        if ((t + 1) * kBN <= Lk) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int r = 4 * (wave + 8 * j) + dma_row;
-                int gk = t * kBN + k_row_of(r);
-                gk = gk < Lk ? gk : Lk - 1;
-                dma16(kbase + (int64_t)gk * a.k_nb1 + ((dma_pc ^ (r & 15)) << 4),
-                      dK + (wave + 8 * j) * 1024);
+            for (int j = 0; j < kRounds; ++j) dma16(vt, v_dma[j], dV + (wave + kWaves * j) * 1024);
+        } else {
+#pragma unroll
+            for (int j = 0; j < kRounds; ++j) {
+                const int r = 4 * (wave + kWaves * j) + dma_row;
+                const int vr = t * kBN + r < Lk ? r : Lk - 1 - t * kBN;
+                dma16(vt, (uint32_t)vr * (uint32_t)a.v_nb1 + ((dma_pc ^ v_swz(r)) << 4),
+                      dV + (wave + kWaves * j) * 1024);
             }
         }
     };
+    auto issue_k = [&](int t, lds_t *dK) {   // K without RoPE
+        const char *kt = kbase + (int64_t)t * kBN * a.k_nb1;
+        if ((t + 1) * kBN <= Lk) {
+#pragma unroll
+            for (int j = 0; j < kRounds; ++j) dma16(kt, k_dma[j], dK + (wave + kWaves * j) * 1024);
+        } else {
+#pragma unroll
+            for (int j = 0; j < kRounds; ++j) {
+                const int r = 4 * (wave + kWaves * j) + dma_row;
+                const int kr = t * kBN + k_row_of(r) < Lk ? k_row_of(r) : Lk - 1 - t * kBN;
+                dma16(kt, (uint32_t)kr * (uint32_t)a.k_nb1 + ((dma_pc ^ (r & 15)) << 4),
+                      dK + (wave + kWaves * j) * 1024);
+            }
+        }
+    };
+    auto issue_tile = [&](int t, lds_t *dK, lds_t *dV) {
+        issue_v(t, dV);
+        if (!ROPE) issue_k(t, dK);
+    };
     // RoPE: K chunk u = tid + 512*j -> LDS row u/16, physical chunk u%16.
-    u32x4 kreg[2];
-    f32x4 kcs[2][2];
+    u32x4 kreg[kRounds];
+    f32x4 kcs[kRounds][2];
     auto rope_load = [&](int t) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < kRounds; ++j) {
             const int u = tid + kThreads * j;
             const int r = u >> 4;
             const int c = (u & 15) ^ (r & 15);
@@ -281,16 +357,16 @@ __global__ __launch_bounds__(kThreads) void fa_fwd_d128(Args a) {
             kcs[j][1] = *reinterpret_cast<const f32x4 *>(cp + 4);
         }
     };
-    auto rope_store = [&](char *dK) {
+    auto rope_store = [&](lds_t *dK) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < kRounds; ++j) {
             const int u = tid + kThreads * j;
             float x[8];
             for (int e = 0; e < 4; ++e) { x[2 * e] = E::lo(kreg[j][e]); x[2 * e + 1] = E::hi(kreg[j][e]); }
             rotate8(x, kcs[j][0], kcs[j][1]);
             u32x4 w;
             for (int e = 0; e < 4; ++e) w[e] = E::pack2(x[2 * e], x[2 * e + 1]);
-            *reinterpret_cast<u32x4 *>(dK + u * 16) = w;
+            *reinterpret_cast<__attribute__((address_space(3))) u32x4 *>(dK + u * 16) = w;
         }
     };
 
@@ -315,38 +391,198 @@ __global__ __launch_bounds__(kThreads) void fa_fwd_d128(Args a) {
             }
     };
 
-    const int n_tiles = (Lk + kBN - 1) / kBN;
-    if (n_tiles > 0) {
-        issue_tile(0, sK0, sV0);
-        if (ROPE) {
-            rope_load(0);
-            rope_store(sK0);
-        }
-        if (HAS_MASK) mask_load(0);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-
     const float c2 = __builtin_fabsf(a.scale_log2);
-    // K-operand LDS offset of this lane (rows l32 and 32 + l32 share the swizzle)
-    const int k_off = l32 * 256;
-    const int k_swz = lane & 15;
-    // V-operand (ds_read_b64_tr_b16) LDS offsets of this lane
-    const int v_sub = (lane & 15) >> 2;            // row within a 4-row group
-    const int v_g1 = (lane >> 4) & 1;
-    const int v_c_lo = 2 * v_g1 + ((lane & 3) >> 1);
-    const int v_byte = 8 * (lane & 1);
+    // K-operand LDS offsets of this lane, one per 16-wide k-step (rows l32
+    // and 32 + l32 share the swizzle)
+    uint32_t k_rd[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) k_rd[ks] = l32 * 256 + (((2 * ks + hi) ^ (lane & 15)) << 4);
+    // V-operand (ds_read_b64_tr_b16) LDS offsets of this lane, one per
+    // 32-wide d block: row 16*kst + 8*hi + v_sub (+4), chunk 4*dblk + v_c_lo;
+    // the swizzle depends on the row only through v_sub
+    const int v_sub = (lane & 15) >> 2;
+    const int v_c_lo = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+    uint32_t v_rd[4];
+#pragma unroll
+    for (int dblk = 0; dblk < 4; ++dblk)
+        v_rd[dblk] = 2048 * hi + 256 * v_sub + (((4 * dblk + v_c_lo) ^ v_swz(v_sub)) << 4) + 8 * (lane & 1);
 
-    auto step = [&](int t, const char *ks_, const char *vs_, char *nK, char *nV) {
-        const bool has_next = t + 1 < n_tiles;
-        if (has_next) {
-            issue_tile(t + 1, nK, nV);
-            if (ROPE) rope_load(t + 1);
+    // ---- S^T = K Q^T for one 64-key tile ---------------------------------------
+    auto qk = [&](const lds_t *ks_, f32x16 &s0, f32x16 &s1) {
+        s0 = (f32x16){};
+        s1 = (f32x16){};
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            const vec8 a0 = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks]);
+            const vec8 a1 = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks] + 32 * 256);
+            s0 = E::mfma(a0, qf[ks], s0);
+            s1 = E::mfma(a1, qf[ks], s1);
         }
+    };
 
-        float mv[32];
-        bool live = true;
-        if (HAS_MASK) {
+    // rescale O and the sums when the running max moves by more than kTau
+    auto update_max = [&](float mx) {
+        if (__builtin_amdgcn_ballot_w64(mx > m_run + kTau) != 0) {
+            const float m_new = __builtin_fmaxf(m_run, mx);
+            const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            l_half *= alpha;
+#pragma unroll
+            for (int dblk = 0; dblk < 4; ++dblk)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[dblk][i] *= alpha;
+        }
+    };
+
+    // P rounded to the operand type (the PV B operands); the row sum uses
+    // the same rounded weights as the numerator
+    auto pack_sum = [&](const float *p, vec8 pb[4]) -> float {
+        float sum = 0.0f;
+#pragma unroll
+        for (int kst = 0; kst < 4; ++kst) {
+            u32x4 w;
+            for (int j = 0; j < 4; ++j) {
+                w[j] = E::pack2(p[8 * kst + 2 * j], p[8 * kst + 2 * j + 1]);
+                sum = E::sum2(w[j], sum);
+            }
+            pb[kst] = __builtin_bit_cast(vec8, w);
+        }
+        return sum;
+    };
+    auto pack_p = [&](const float *p, vec8 pb[4]) { l_half += pack_sum(p, pb); };
+
+    // online softmax with the additive mask: logits s*c2 + mask*log2(e);
+    // -inf mask entries (and keys past Lk, filled with -inf) stay -inf
+    auto softmax_masked = [&](const f32x16 &s0, const f32x16 &s1, const float *mv, vec8 pb[4]) {
+        float p[32];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            p[i] = s0[i];
+            p[16 + i] = s1[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 32; ++i)
+            p[i] = mv[i] == -INFINITY ? -INFINITY : __builtin_fmaf(mv[i], kLog2e, p[i] * c2);
+        update_max(pair_max(max32(p)));
+        const float mu = m_run == -INFINITY ? 0.0f : m_run;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) p[i] = __builtin_amdgcn_exp2f(p[i] - mu);
+        pack_p(p, pb);
+    };
+
+    // ---- O^T += V^T P^T ------------------------------------------------------
+    auto pv = [&](const lds_t *vs_, const vec8 pb[4]) {
+#pragma unroll
+        for (int kst = 0; kst < 4; ++kst) {
+#pragma unroll
+            for (int dblk = 0; dblk < 4; ++dblk) {
+                const lds_t *vp = vs_ + v_rd[dblk] + 4096 * kst;
+                const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(vp));
+                const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(vp + 1024));
+                const vec8 va = __builtin_bit_cast(vec8, __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+                o[dblk] = E::mfma(va, pb[kst], o[dblk]);
+            }
+        }
+    };
+
+    auto load_tile_sync = [&](int t, lds_t *dK, lds_t *dV) {
+        issue_tile(t, dK, dV);
+        if (ROPE) {
+            rope_load(t);
+            rope_store(dK);
+        }
+    };
+
+    const int n_tiles = (Lk + kBN - 1) / kBN;
+
+    if constexpr (!HAS_MASK) {
+        // Two LDS stages; tile t+1 streams in while tile t is computed.
+        // The running max m_run is not refreshed every tile: the exponents
+        // of tile t are taken against the current m_run, and only when a
+        // row's sum of weights leaves [0, 2^kSumCap] (a score far above
+        // m_run, or the first tile with m_run = -inf) is the tile's exact
+        // row max computed, O rescaled and the exponents redone.  Weights
+        // stay <= 2^kSumCap, far inside the F32 / bf16 range.
+        if (n_tiles > 0) load_tile_sync(0, sK0, sV0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        auto step = [&](int t, const lds_t *ks_, const lds_t *vs_, lds_t *nK, lds_t *nV) {
+            const bool has_next = t + 1 < n_tiles;
+            if (has_next) {
+                issue_tile(t + 1, nK, nV);
+                if (ROPE) rope_load(t + 1);
+            }
+            f32x16 s0, s1;
+            KD_FA_PRIO(1);
+            qk(ks_, s0, s1);
+            KD_FA_PRIO(0);
+            // keys past Lk (last tile only) read clamped K rows, i.e. copies
+            // of key Lk-1: finite scores that never raise the row max; their
+            // weights are zeroed after the exponent
+            const bool tail = (t + 1) * kBN > Lk;
+            auto drop_tail = [&](float *p) {
+                if (tail) {
+#pragma unroll
+                    for (int i = 0; i < 32; ++i) {
+                        const int key = t * kBN + (i >> 4) * 32 + 16 * ((i >> 3) & 1) + 8 * hi + (i & 7);
+                        p[i] = key < Lk ? p[i] : 0.0f;
+                    }
+                }
+            };
+            vec8 pb[4];
+            float p[32];
+            float nm = -m_run;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], c2, nm));
+                p[16 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], c2, nm));
+            }
+            drop_tail(p);
+            float sum = pack_sum(p, pb);
+            const float pair = pair_sum(sum);
+            // !(x <= cap) also catches NaN (inf - inf with m_run = -inf)
+            if (__builtin_amdgcn_ballot_w64(!(pair <= kSumCap)) != 0) {
+                float q[32];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) { q[i] = s0[i]; q[16 + i] = s1[i]; }
+                update_max(pair_max(max32(q)) * c2);
+                nm = -m_run;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], c2, nm));
+                    p[16 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], c2, nm));
+                }
+                drop_tail(p);
+                sum = pack_sum(p, pb);
+            }
+            l_half += sum;
+            KD_FA_PRIO(1);
+            pv(vs_, pb);
+            KD_FA_PRIO(0);
+            if (ROPE && has_next) rope_store(nK);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+        };
+        for (int t = 0; t < n_tiles; t += 2) {
+            step(t, sK0, sV0, sK1, sV1);
+            if (t + 1 < n_tiles) step(t + 1, sK1, sV1, sK0, sV0);
+        }
+    } else {
+        // masked: two LDS stages; a tile whose mask is -inf for all of this
+        // wave's rows is skipped (no MFMA, no softmax)
+        if (n_tiles > 0) {
+            load_tile_sync(0, sK0, sV0);
+            mask_load(0);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        auto mstep = [&](int t, const lds_t *ks_, const lds_t *vs_, lds_t *nK, lds_t *nV) {
+            const bool has_next = t + 1 < n_tiles;
+            if (has_next) {
+                issue_tile(t + 1, nK, nV);
+                if (ROPE) rope_load(t + 1);
+            }
+            float mv[32];
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4)
 #pragma unroll
@@ -357,130 +593,23 @@ __global__ __launch_bounds__(kThreads) void fa_fwd_d128(Args a) {
             bool any = false;
 #pragma unroll
             for (int i = 0; i < 32; ++i) any |= mv[i] != -INFINITY;
-            live = __builtin_amdgcn_ballot_w64(any) != 0;
+            const bool live = __builtin_amdgcn_ballot_w64(any) != 0;
             if (has_next) mask_load(t + 1);
+            if (live) {
+                f32x16 s0, s1;
+                qk(ks_, s0, s1);
+                vec8 pb[4];
+                softmax_masked(s0, s1, mv, pb);
+                pv(vs_, pb);
+            }
+            if (ROPE && has_next) rope_store(nK);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+        };
+        for (int t = 0; t < n_tiles; t += 2) {
+            mstep(t, sK0, sV0, sK1, sV1);
+            if (t + 1 < n_tiles) mstep(t + 1, sK1, sV1, sK0, sV0);
         }
-
-        if (live) {
-            // ---- S^T = K Q^T ------------------------------------------------
-            f32x16 s0 = (f32x16){}, s1 = (f32x16){};
-#pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
-                const int off = k_off + (((2 * ks + hi) ^ k_swz) << 4);
-                const vec8 a0 = *reinterpret_cast<const vec8 *>(ks_ + off);
-                const vec8 a1 = *reinterpret_cast<const vec8 *>(ks_ + off + 32 * 256);
-                s0 = E::mfma(a0, qf[ks], s0);
-                s1 = E::mfma(a1, qf[ks], s1);
-            }
-
-            // ---- online softmax (log2 domain) -------------------------------
-            float p[32];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                p[i] = s0[i];
-                p[16 + i] = s1[i];
-            }
-            if (!HAS_MASK) {
-                // keys past Lk (last tile only): -inf raw scores for the max
-                // (each lane pair still holds the tile's first key, which is
-                // valid) and -inf exponents below
-                const bool tail = (t + 1) * kBN > Lk;
-                if (tail) {
-#pragma unroll
-                    for (int i = 0; i < 32; ++i) {
-                        const int key = t * kBN + (i >> 4) * 32 + 16 * ((i >> 3) & 1) + 8 * hi + (i & 7);
-                        p[i] = key < Lk ? p[i] : -INFINITY;
-                    }
-                }
-                float mx = max3(p[0], p[1], p[2]);
-#pragma unroll
-                for (int i = 3; i < 31; i += 2) mx = max3(mx, p[i], p[i + 1]);
-                mx = __builtin_fmaxf(mx, p[31]);
-                mx = pair_max(mx) * c2;
-                if (__builtin_amdgcn_ballot_w64(mx > m_run + kTau) != 0) {
-                    const float m_new = __builtin_fmaxf(m_run, mx);
-                    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-                    m_run = m_new;
-                    l_half *= alpha;
-#pragma unroll
-                    for (int dblk = 0; dblk < 4; ++dblk)
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) o[dblk][i] *= alpha;
-                }
-                const float nm = -m_run;
-#pragma unroll
-                for (int i = 0; i < 32; ++i) p[i] = __builtin_fmaf(p[i], c2, nm);
-                if (tail) {
-#pragma unroll
-                    for (int i = 0; i < 32; ++i) {
-                        const int key = t * kBN + (i >> 4) * 32 + 16 * ((i >> 3) & 1) + 8 * hi + (i & 7);
-                        p[i] = key < Lk ? p[i] : -INFINITY;
-                    }
-                }
-#pragma unroll
-                for (int i = 0; i < 32; ++i) p[i] = __builtin_amdgcn_exp2f(p[i]);
-            } else {
-                // log2-domain logits s*c2 + mask*log2(e); -inf mask entries
-                // (and keys past Lk, filled with -inf) stay -inf
-#pragma unroll
-                for (int i = 0; i < 32; ++i)
-                    p[i] = mv[i] == -INFINITY ? -INFINITY : __builtin_fmaf(mv[i], kLog2e, p[i] * c2);
-                float mx = max3(p[0], p[1], p[2]);
-#pragma unroll
-                for (int i = 3; i < 31; i += 2) mx = max3(mx, p[i], p[i + 1]);
-                mx = __builtin_fmaxf(mx, p[31]);
-                mx = pair_max(mx);
-                if (__builtin_amdgcn_ballot_w64(mx > m_run + kTau) != 0) {
-                    const float m_new = __builtin_fmaxf(m_run, mx);
-                    const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-                    m_run = m_new;
-                    l_half *= alpha;
-#pragma unroll
-                    for (int dblk = 0; dblk < 4; ++dblk)
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) o[dblk][i] *= alpha;
-                }
-                const float mu = m_run == -INFINITY ? 0.0f : m_run;
-#pragma unroll
-                for (int i = 0; i < 32; ++i) p[i] = __builtin_amdgcn_exp2f(p[i] - mu);
-            }
-            float sum = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 32; ++i) sum += p[i];
-            l_half += sum;
-
-            // ---- O^T += V^T P^T ----------------------------------------------
-            vec8 pb[4];
-#pragma unroll
-            for (int kst = 0; kst < 4; ++kst) {
-                u32x4 w;
-                for (int j = 0; j < 4; ++j) w[j] = E::pack2(p[8 * kst + 2 * j], p[8 * kst + 2 * j + 1]);
-                pb[kst] = __builtin_bit_cast(vec8, w);
-            }
-#pragma unroll
-            for (int kst = 0; kst < 4; ++kst) {
-#pragma unroll
-                for (int dblk = 0; dblk < 4; ++dblk) {
-                    const int c = 4 * dblk + v_c_lo;
-                    const int r0 = 16 * kst + 8 * hi + v_sub;
-                    const int r1 = r0 + 4;
-                    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        LDS_PTR(s16x4, vs_ + r0 * 256 + ((c ^ v_swz(r0)) << 4) + v_byte));
-                    const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        LDS_PTR(s16x4, vs_ + r1 * 256 + ((c ^ v_swz(r1)) << 4) + v_byte));
-                    const vec8 va = __builtin_bit_cast(vec8, __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
-                    o[dblk] = E::mfma(va, pb[kst], o[dblk]);
-                }
-            }
-        }
-
-        if (ROPE && has_next) rope_store(nK);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-    };
-    for (int t = 0; t < n_tiles; t += 2) {
-        step(t, sK0, sV0, sK1, sV1);
-        if (t + 1 < n_tiles) step(t + 1, sK1, sV1, sK0, sV0);
     }
 
     // ---- epilogue: O / l -> dst[b][q][h][:] (F32) ---------------------------

@@ -26,7 +26,8 @@ import os
 import re
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libkd_fa.so")
+# KD_FA_LIB selects another build of the same library (e.g. a tuning variant)
+LIB_PATH = os.environ.get("KD_FA_LIB") or os.path.join(_HERE, "libkd_fa.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "kd_fa.h")
 
 TYPE_F32 = 0
