@@ -153,6 +153,24 @@ int kd_fa_run(const kd_fa_desc *desc, void *stream);
 int kd_fa_rope_run(const kd_fa_desc *desc, const kd_fa_rope *rope, void *stream);
 
 /*
+ * kd_fa_rope_run_ws - kd_fa_rope_run for callers that can lend a K-sized
+ * buffer (in a ggml graph: the tensor the unfused graph casts the rotated
+ * K into, src/core/ops.hpp:167): K is rotated once per call into
+ * `workspace` (contiguous [Dk, Lk, Hkv, Bk] in K's type) by a separate
+ * pass on `stream`, and the attention then rotates only Q on load.  The
+ * result is bitwise equal to kd_fa_rope_run's; the workspace holds the
+ * rotated K afterwards.  workspace_bytes must be at least
+ * kd_fa_rope_workspace_size(desc) and workspace 16-byte aligned
+ * (KD_FA_ERR_LAYOUT otherwise, KD_FA_ERR_NULL when it is NULL).  The library
+ * still allocates nothing.
+ */
+int kd_fa_rope_run_ws(const kd_fa_desc *desc, const kd_fa_rope *rope, void *workspace,
+                      size_t workspace_bytes, void *stream);
+
+/* Bytes of K-sized workspace kd_fa_rope_run_ws needs (0 for an invalid node). */
+size_t kd_fa_rope_workspace_size(const kd_fa_desc *desc);
+
+/*
  * kd_fa_rope_supports - kd_fa_supports plus the checks of the RoPE
  * descriptor.  Host-only.
  */

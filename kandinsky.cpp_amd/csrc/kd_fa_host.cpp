@@ -16,6 +16,8 @@ namespace {
 
 constexpr int64_t kHeadDim = 128;
 constexpr int64_t kI32Max = 0x7fffffff;
+// A 64-row tile is addressed with 32-bit offsets from a per-tile base.
+constexpr uint64_t kMaxRowStride = (uint64_t)1 << 25;
 
 size_t elem_size(int type) { return type == KD_FA_TYPE_F32 ? 4 : 2; }
 bool is_16b(uint64_t x) { return (x & 15u) == 0; }
@@ -60,6 +62,7 @@ int validate(const kd_fa_desc *d, const kd_fa_rope *r, bool *mask_vec) {
     const kd_fa_tensor *vec_t[4] = {&q, &k, &v, &o};
     for (const kd_fa_tensor *t : vec_t) {
         if (t->nb[0] != elem_size(t->type)) return KD_FA_ERR_LAYOUT;
+        if (t->nb[1] > kMaxRowStride) return KD_FA_ERR_LAYOUT;
         if (!is_16b(t->data) || !is_16b(t->nb[1]) || !is_16b(t->nb[2]) || !is_16b(t->nb[3])) return KD_FA_ERR_LAYOUT;
     }
     bool mv = false;
@@ -78,6 +81,7 @@ int validate(const kd_fa_desc *d, const kd_fa_rope *r, bool *mask_vec) {
             if (!t.data || t.type != KD_FA_TYPE_F32) return KD_FA_ERR_ROPE;
             if (t.ne[0] != kHeadDim || t.ne[1] < L || t.nb[0] != 4) return KD_FA_ERR_ROPE;
             if (!is_16b(t.data) || !is_16b(t.nb[1])) return KD_FA_ERR_ROPE;
+            if (t.nb[1] > kMaxRowStride) return KD_FA_ERR_ROPE;
         } else if (r->mode == KD_FA_ROPE_AXES) {
             if (!r->axes_data || !is_16b(r->axes_data)) return KD_FA_ERR_ROPE;
             for (int i = 0; i < 3; ++i) {
@@ -86,7 +90,7 @@ int validate(const kd_fa_desc *d, const kd_fa_rope *r, bool *mask_vec) {
             }
             if (r->axes[0] + r->axes[1] + r->axes[2] != kHeadDim) return KD_FA_ERR_ROPE;
             const int64_t cells = (int64_t)r->grid[0] * r->grid[1] * r->grid[2];
-            if (cells < L || cells > kI32Max) return KD_FA_ERR_ROPE;
+            if (cells < L || L > (int64_t)1 << 24) return KD_FA_ERR_ROPE;
         } else {
             return KD_FA_ERR_ROPE;
         }
@@ -113,10 +117,21 @@ int device_ok() {
     return st == 1 ? KD_FA_OK : KD_FA_ERR_DEVICE;
 }
 
-int run(const kd_fa_desc *d, const kd_fa_rope *r, void *stream) {
+size_t rope_ws_bytes(const kd_fa_desc *d) {
+    return (size_t)kHeadDim * (size_t)d->k.ne[1] * (size_t)d->k.ne[2] * (size_t)d->k.ne[3] *
+           elem_size(d->k.type);
+}
+
+// ws != nullptr: rotate K once into ws (contiguous, K's type) and run the
+// attention with only Q rotated on load.
+int run(const kd_fa_desc *d, const kd_fa_rope *r, void *ws, size_t ws_bytes, void *stream) {
     bool mask_vec = false;
     int st = validate(d, r, &mask_vec);
     if (st != KD_FA_OK) return st;
+    const bool rope_on = r && r->mode != KD_FA_ROPE_NONE;
+    if (ws && rope_on) {
+        if (!is_16b(ws) || ws_bytes < rope_ws_bytes(d)) return KD_FA_ERR_LAYOUT;
+    }
     const int64_t Lq = d->q.ne[1], H = d->q.ne[2], B = d->q.ne[3];
     if (Lq == 0 || H == 0 || B == 0) return KD_FA_OK;
     st = device_ok();
@@ -154,11 +169,25 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, void *stream) {
         a.axes = r->axes_data;
         a.grid_t = r->grid[0]; a.grid_h = r->grid[1]; a.grid_w = r->grid[2];
         a.axis0 = r->axes[0]; a.axis1 = r->axes[1]; a.axis2 = r->axes[2];
+        a.rcp_h = 1.0f / (float)r->grid[1];
+        a.rcp_w = 1.0f / (float)r->grid[2];
     }
     a.n_qt = (int32_t)((Lq + kdfa::kBlockM - 1) / kdfa::kBlockM);
     a.n_blocks = (int32_t)(a.n_qt * H * B);
 
-    if (kdfa::launch(a, d->k.type, static_cast<hipStream_t>(stream)) != hipSuccess) return KD_FA_ERR_LAUNCH;
+    hipStream_t hs = static_cast<hipStream_t>(stream);
+    bool k_rope = rope_on;
+    if (ws && rope_on) {
+        const int hk = (int)d->k.ne[2], bk = (int)d->k.ne[3];
+        if (kdfa::launch_rope_k(a, d->k.type, hk, bk, ws, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
+        const int64_t row = kHeadDim * (int64_t)elem_size(d->k.type);
+        a.k = static_cast<const char *>(ws);
+        a.k_nb1 = row;
+        a.k_nb2 = row * a.Lk;
+        a.k_nb3 = row * a.Lk * hk;
+        k_rope = false;
+    }
+    if (kdfa::launch(a, d->k.type, k_rope, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
     return KD_FA_OK;
 }
 
@@ -190,10 +219,22 @@ int kd_fa_rope_supports(const kd_fa_desc *desc, const kd_fa_rope *rope, int *rea
     return st == KD_FA_OK ? 1 : 0;
 }
 
-int kd_fa_run(const kd_fa_desc *desc, void *stream) { return run(desc, nullptr, stream); }
+int kd_fa_run(const kd_fa_desc *desc, void *stream) { return run(desc, nullptr, nullptr, 0, stream); }
 
 int kd_fa_rope_run(const kd_fa_desc *desc, const kd_fa_rope *rope, void *stream) {
-    return run(desc, rope, stream);
+    return run(desc, rope, nullptr, 0, stream);
+}
+
+size_t kd_fa_rope_workspace_size(const kd_fa_desc *desc) {
+    if (!desc || validate(desc, nullptr, nullptr) != KD_FA_OK) return 0;
+    return rope_ws_bytes(desc);
+}
+
+int kd_fa_rope_run_ws(const kd_fa_desc *desc, const kd_fa_rope *rope, void *workspace,
+                      size_t workspace_bytes, void *stream) {
+    if (!workspace && rope && rope->mode != KD_FA_ROPE_NONE && desc && desc->k.ne[1] > 0)
+        return KD_FA_ERR_NULL;
+    return run(desc, rope, workspace, workspace_bytes, stream);
 }
 
 // rope::compute_visual_rope (src/rope.hpp:56-102).

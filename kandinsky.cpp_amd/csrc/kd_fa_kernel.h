@@ -35,12 +35,18 @@ struct Args {
     const float *axes;
     int32_t grid_t, grid_h, grid_w;
     int32_t axis0, axis1, axis2;
+    float rcp_h, rcp_w;   // 1.0f / grid_h, 1.0f / grid_w
     int32_t n_qt;       // query tiles per (b, h)
     int32_t n_blocks;   // n_qt * H * B
 };
 
 // Enqueue the forward kernel for K/V element type kv_type on `stream`.
-hipError_t launch(const Args &a, int kv_type, hipStream_t stream);
+// With a RoPE mode set, Q is rotated on load, and K too when k_rope.
+hipError_t launch(const Args &a, int kv_type, bool k_rope, hipStream_t stream);
+
+// Rotate K ([D, Lk, H/rk2, B/rk3] through a.k and its strides) into `out`,
+// contiguous, in K's type.
+hipError_t launch_rope_k(const Args &a, int kv_type, int k_heads, int k_batch, void *out, hipStream_t stream);
 
 // Waves per workgroup (32 query rows each).
 #ifndef KD_FA_WAVES

@@ -142,17 +142,31 @@ static __device__ __forceinline__ void load8_f32(const char *p, int type, float 
     }
 }
 
-// Address of the (cos, sin) pairs for columns d0 .. d0+7 of token `tok`.
+// n / d for 0 <= n < 2^24, d >= 1, given rd = 1.0f / d: the float quotient
+// is within one of the true one, and one correction step each way fixes it.
+static __device__ __forceinline__ int div_small(int n, int d, float rd) {
+    int q = (int)((float)n * rd);
+    const int r = n - q * d;
+    q += (r >= d) - (r < 0);
+    return q;
+}
+
+// (cos, sin) pairs for columns d0 .. d0+7 of token `tok`: TABLE reads row
+// `tok` of the [D, L] table; AXES reads the row of the token's t, h or w
+// coordinate from the per-axis table holding that column block.
+template <int RM>
 static __device__ __forceinline__ const float *rope_ptr(const Args &a, int tok, int d0) {
-    if (a.rope_mode == KD_FA_ROPE_TABLE)
+    if (RM == KD_FA_ROPE_TABLE)
         return reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.rope_tab) +
                                                (int64_t)tok * a.rope_nb1) + d0;
-    const int hw = a.grid_h * a.grid_w;
-    if (d0 < a.axis0) return a.axes + (tok / hw) * a.axis0 + d0;
-    if (d0 < a.axis0 + a.axis1)
-        return a.axes + a.grid_t * a.axis0 + ((tok / a.grid_w) % a.grid_h) * a.axis1 + (d0 - a.axis0);
-    return a.axes + a.grid_t * a.axis0 + a.grid_h * a.axis1 + (tok % a.grid_w) * a.axis2 +
-           (d0 - a.axis0 - a.axis1);
+    const int tw = div_small(tok, a.grid_w, a.rcp_w);          // t*Hp + h
+    if (d0 < a.axis0) return a.axes + div_small(tw, a.grid_h, a.rcp_h) * a.axis0 + d0;
+    if (d0 < a.axis0 + a.axis1) {
+        const int h = tw - div_small(tw, a.grid_h, a.rcp_h) * a.grid_h;
+        return a.axes + a.grid_t * a.axis0 + h * a.axis1 + (d0 - a.axis0);
+    }
+    const int w = tok - tw * a.grid_w;
+    return a.axes + a.grid_t * a.axis0 + a.grid_h * a.axis1 + w * a.axis2 + (d0 - a.axis0 - a.axis1);
 }
 
 // rope::apply's pair rotation (src/rope.hpp:137-138): every product and
@@ -219,9 +233,11 @@ static __device__ __forceinline__ float pair_sum(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <typename T, bool HAS_MASK, bool ROPE>
+template <typename T, bool HAS_MASK, int RM, bool KROPE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void fa_fwd_d128(Args a) {
+    constexpr bool ROPE = RM != KD_FA_ROPE_NONE;   // rotate Q on load
+    constexpr bool KR = ROPE && KROPE;              // rotate K tiles on load
     typedef Elem<T> E;
     typedef typename E::vec8 vec8;
     // four distinct LDS objects (not one array) so that the compiler can
@@ -267,7 +283,7 @@ void fa_fwd_d128(Args a) {
             float x[8];
             load8_f32(qp + d0 * esz, a.q_type, x);
             if (ROPE) {
-                const float *cp = rope_ptr(a, q_ld, d0);
+                const float *cp = rope_ptr<RM>(a, q_ld, d0);
                 rotate8(x, *reinterpret_cast<const f32x4 *>(cp), *reinterpret_cast<const f32x4 *>(cp + 4));
             }
             u32x4 w;
@@ -338,23 +354,41 @@ void fa_fwd_d128(Args a) {
     };
     auto issue_tile = [&](int t, lds_t *dK, lds_t *dV) {
         issue_v(t, dV);
-        if (!ROPE) issue_k(t, dK);
+        if (!KR) issue_k(t, dK);
     };
-    // RoPE: K chunk u = tid + 512*j -> LDS row u/16, physical chunk u%16.
+    // RoPE: K chunk u = tid + kThreads*j -> LDS row u/16, physical chunk
+    // u%16 -- the same rows and chunks as the DMA lanes, so the K source
+    // offsets are k_dma[]; TABLE mode reads the table row of the same key.
     u32x4 kreg[kRounds];
     f32x4 kcs[kRounds][2];
+    uint32_t tab_off[kRounds];
+#pragma unroll
+    for (int j = 0; j < kRounds; ++j) {
+        const int r = 4 * (wave + kWaves * j) + dma_row;
+        tab_off[j] = (uint32_t)k_row_of(r) * (uint32_t)a.rope_nb1 + (((dma_pc ^ (r & 15)) << 5));
+    }
     auto rope_load = [&](int t) {
+        const char *kt = kbase + (int64_t)t * kBN * a.k_nb1;
+        const bool full = (t + 1) * kBN <= Lk;
 #pragma unroll
         for (int j = 0; j < kRounds; ++j) {
-            const int u = tid + kThreads * j;
-            const int r = u >> 4;
-            const int c = (u & 15) ^ (r & 15);
-            int gk = t * kBN + k_row_of(r);
-            gk = gk < Lk ? gk : Lk - 1;
-            kreg[j] = ld16(kbase + (int64_t)gk * a.k_nb1 + c * 16);
-            const float *cp = rope_ptr(a, gk, c * 8);
-            kcs[j][0] = *reinterpret_cast<const f32x4 *>(cp);
-            kcs[j][1] = *reinterpret_cast<const f32x4 *>(cp + 4);
+            const int r = 4 * (wave + kWaves * j) + dma_row;
+            const int c = dma_pc ^ (r & 15);
+            int kr = k_row_of(r);
+            if (!full && t * kBN + kr >= Lk) kr = Lk - 1 - t * kBN;
+            if (RM == KD_FA_ROPE_TABLE) {
+                const char *tt = reinterpret_cast<const char *>(a.rope_tab) + (int64_t)t * kBN * a.rope_nb1;
+                const uint32_t ko = full ? k_dma[j] : (uint32_t)kr * (uint32_t)a.k_nb1 + (c << 4);
+                const uint32_t to = full ? tab_off[j] : (uint32_t)kr * (uint32_t)a.rope_nb1 + (c << 5);
+                kreg[j] = ld16(kt + ko);
+                kcs[j][0] = *reinterpret_cast<const f32x4 *>(tt + to);
+                kcs[j][1] = *reinterpret_cast<const f32x4 *>(tt + to + 16);
+            } else {
+                kreg[j] = ld16(kt + ((uint32_t)kr * (uint32_t)a.k_nb1 + (c << 4)));
+                const float *cp = rope_ptr<RM>(a, t * kBN + kr, c * 8);
+                kcs[j][0] = *reinterpret_cast<const f32x4 *>(cp);
+                kcs[j][1] = *reinterpret_cast<const f32x4 *>(cp + 4);
+            }
         }
     };
     auto rope_store = [&](lds_t *dK) {
@@ -487,7 +521,7 @@ void fa_fwd_d128(Args a) {
 
     auto load_tile_sync = [&](int t, lds_t *dK, lds_t *dV) {
         issue_tile(t, dK, dV);
-        if (ROPE) {
+        if (KR) {
             rope_load(t);
             rope_store(dK);
         }
@@ -510,7 +544,7 @@ void fa_fwd_d128(Args a) {
             const bool has_next = t + 1 < n_tiles;
             if (has_next) {
                 issue_tile(t + 1, nK, nV);
-                if (ROPE) rope_load(t + 1);
+                if (KR) rope_load(t + 1);
             }
             f32x16 s0, s1;
             KD_FA_PRIO(1);
@@ -559,7 +593,7 @@ void fa_fwd_d128(Args a) {
             KD_FA_PRIO(1);
             pv(vs_, pb);
             KD_FA_PRIO(0);
-            if (ROPE && has_next) rope_store(nK);
+            if (KR && has_next) rope_store(nK);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
         };
@@ -580,7 +614,7 @@ void fa_fwd_d128(Args a) {
             const bool has_next = t + 1 < n_tiles;
             if (has_next) {
                 issue_tile(t + 1, nK, nV);
-                if (ROPE) rope_load(t + 1);
+                if (KR) rope_load(t + 1);
             }
             float mv[32];
 #pragma unroll
@@ -602,7 +636,7 @@ void fa_fwd_d128(Args a) {
                 softmax_masked(s0, s1, mv, pb);
                 pv(vs_, pb);
             }
-            if (ROPE && has_next) rope_store(nK);
+            if (KR && has_next) rope_store(nK);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
         };
@@ -629,23 +663,77 @@ void fa_fwd_d128(Args a) {
     }
 }
 
-template <typename T, bool M, bool R>
+template <typename T, bool M, int R, bool KR>
 static hipError_t launch_t(const Args &a, hipStream_t stream) {
-    hipLaunchKernelGGL((fa_fwd_d128<T, M, R>), dim3(a.n_blocks), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((fa_fwd_d128<T, M, R, KR>), dim3(a.n_blocks), dim3(kThreads), 0, stream, a);
     return hipGetLastError();
 }
 
-template <typename T>
-static hipError_t launch_m(const Args &a, bool mask, bool rope, hipStream_t s) {
-    if (mask) return rope ? launch_t<T, true, true>(a, s) : launch_t<T, true, false>(a, s);
-    return rope ? launch_t<T, false, true>(a, s) : launch_t<T, false, false>(a, s);
+template <typename T, bool M>
+static hipError_t launch_r(const Args &a, bool k_rope, hipStream_t s) {
+    switch (a.rope_mode) {
+    case KD_FA_ROPE_TABLE:
+        return k_rope ? launch_t<T, M, KD_FA_ROPE_TABLE, true>(a, s) : launch_t<T, M, KD_FA_ROPE_TABLE, false>(a, s);
+    case KD_FA_ROPE_AXES:
+        return k_rope ? launch_t<T, M, KD_FA_ROPE_AXES, true>(a, s) : launch_t<T, M, KD_FA_ROPE_AXES, false>(a, s);
+    default:
+        return launch_t<T, M, KD_FA_ROPE_NONE, false>(a, s);
+    }
 }
 
-hipError_t launch(const Args &a, int kv_type, hipStream_t stream) {
+hipError_t launch(const Args &a, int kv_type, bool k_rope, hipStream_t stream) {
     const bool mask = a.m != nullptr;
-    const bool rope = a.rope_mode != KD_FA_ROPE_NONE;
-    if (kv_type == KD_FA_TYPE_BF16) return launch_m<__bf16>(a, mask, rope, stream);
-    return launch_m<_Float16>(a, mask, rope, stream);
+    if (kv_type == KD_FA_TYPE_BF16)
+        return mask ? launch_r<__bf16, true>(a, k_rope, stream) : launch_r<__bf16, false>(a, k_rope, stream);
+    return mask ? launch_r<_Float16, true>(a, k_rope, stream) : launch_r<_Float16, false>(a, k_rope, stream);
+}
+
+// ---------------------------------------------------------------------------
+// K pre-rotation: rope::apply on K (src/rope.hpp:109-155) with the same F32
+// arithmetic as the in-kernel rotation, rounded to K's type, written to a
+// contiguous [D, Lk, Hkv, Bk] buffer.  One thread per 16-byte chunk.
+// ---------------------------------------------------------------------------
+template <typename T, int RM>
+__global__ __launch_bounds__(256) void rope_k_kernel(Args a, char *out, int64_t n_chunks) {
+    typedef Elem<T> E;
+    const int hk = a.H / a.rk2;   // K heads
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_chunks;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int c = (int)(i & 15);
+        const int64_t row = i >> 4;                  // (b, h, key) flattened, key fastest
+        const int key = (int)(row % a.Lk);
+        const int64_t hb = row / a.Lk;
+        const int h = (int)(hb % hk);
+        const int b = (int)(hb / hk);
+        const char *src = a.k + (int64_t)key * a.k_nb1 + (int64_t)h * a.k_nb2 + (int64_t)b * a.k_nb3 + c * 16;
+        u32x4 w = ld16(src);
+        float x[8];
+        for (int e = 0; e < 4; ++e) { x[2 * e] = E::lo(w[e]); x[2 * e + 1] = E::hi(w[e]); }
+        const float *cp = rope_ptr<RM>(a, key, c * 8);
+        rotate8(x, *reinterpret_cast<const f32x4 *>(cp), *reinterpret_cast<const f32x4 *>(cp + 4));
+        for (int e = 0; e < 4; ++e) w[e] = E::pack2(x[2 * e], x[2 * e + 1]);
+        *reinterpret_cast<u32x4 *>(out + i * 16) = w;
+    }
+}
+
+hipError_t launch_rope_k(const Args &a, int kv_type, int k_heads, int k_batch, void *out, hipStream_t stream) {
+    const int64_t n_chunks = (int64_t)a.Lk * k_heads * k_batch * 16;
+    if (n_chunks == 0) return hipSuccess;
+    const int64_t want = (n_chunks + 255) / 256;
+    const int grid = (int)(want < 65536 ? want : 65536);
+    char *o = static_cast<char *>(out);
+    if (kv_type == KD_FA_TYPE_BF16) {
+        if (a.rope_mode == KD_FA_ROPE_TABLE)
+            hipLaunchKernelGGL((rope_k_kernel<__bf16, KD_FA_ROPE_TABLE>), dim3(grid), dim3(256), 0, stream, a, o, n_chunks);
+        else
+            hipLaunchKernelGGL((rope_k_kernel<__bf16, KD_FA_ROPE_AXES>), dim3(grid), dim3(256), 0, stream, a, o, n_chunks);
+    } else {
+        if (a.rope_mode == KD_FA_ROPE_TABLE)
+            hipLaunchKernelGGL((rope_k_kernel<_Float16, KD_FA_ROPE_TABLE>), dim3(grid), dim3(256), 0, stream, a, o, n_chunks);
+        else
+            hipLaunchKernelGGL((rope_k_kernel<_Float16, KD_FA_ROPE_AXES>), dim3(grid), dim3(256), 0, stream, a, o, n_chunks);
+    }
+    return hipGetLastError();
 }
 
 }  // namespace kdfa

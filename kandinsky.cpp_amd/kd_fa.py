@@ -117,6 +117,10 @@ def _lib():
         lib.kd_fa_run.restype = ctypes.c_int
         lib.kd_fa_rope_run.argtypes = [P(KdFaDesc), P(KdFaRope), ctypes.c_void_p]
         lib.kd_fa_rope_run.restype = ctypes.c_int
+        lib.kd_fa_rope_run_ws.argtypes = [P(KdFaDesc), P(KdFaRope), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.kd_fa_rope_run_ws.restype = ctypes.c_int
+        lib.kd_fa_rope_workspace_size.argtypes = [P(KdFaDesc)]
+        lib.kd_fa_rope_workspace_size.restype = ctypes.c_size_t
         fp = P(ctypes.c_float)
         ip = P(ctypes.c_int)
         lib.kd_fa_rope_visual_table.argtypes = [ctypes.c_int] * 3 + [ip, fp, ctypes.c_float, fp]
@@ -246,9 +250,11 @@ def supports(q, k, v, mask=None, dst=None, scale=1.0, max_bias=0.0, logit_softca
     return bool(ok), reason.value
 
 
-def run_desc(desc: KdFaDesc, rope: KdFaRope | None = None, stream=None) -> int:
+def run_desc(desc: KdFaDesc, rope: KdFaRope | None = None, stream=None, workspace=None) -> int:
     """Enqueue on `stream` (a torch.cuda.Stream, a raw handle, or None for
-    torch's current stream).  Returns the status code."""
+    torch's current stream).  With `workspace` (a tensor of at least
+    workspace_size(desc) bytes) the RoPE call pre-rotates K into it
+    (kd_fa_rope_run_ws).  Returns the status code."""
     torch = _torch()
     if stream is None:
         handle = torch.cuda.current_stream().cuda_stream
@@ -258,11 +264,21 @@ def run_desc(desc: KdFaDesc, rope: KdFaRope | None = None, stream=None) -> int:
         handle = stream.cuda_stream
     if rope is None:
         return _lib().kd_fa_run(ctypes.byref(desc), ctypes.c_void_p(handle))
+    if workspace is not None:
+        nbytes = workspace.numel() * workspace.element_size()
+        return _lib().kd_fa_rope_run_ws(ctypes.byref(desc), ctypes.byref(rope),
+                                        ctypes.c_void_p(workspace.data_ptr()), nbytes,
+                                        ctypes.c_void_p(handle))
     return _lib().kd_fa_rope_run(ctypes.byref(desc), ctypes.byref(rope), ctypes.c_void_p(handle))
 
 
+def workspace_size(desc: KdFaDesc) -> int:
+    """kd_fa_rope_workspace_size: bytes of K-sized buffer for kd_fa_rope_run_ws."""
+    return int(_lib().kd_fa_rope_workspace_size(ctypes.byref(desc)))
+
+
 def flash_attn_ext(q, k, v, mask=None, scale=None, max_bias=0.0, logit_softcap=0.0,
-                   dst=None, rope=None, stream=None):
+                   dst=None, rope=None, stream=None, workspace=None):
     """GGML_OP_FLASH_ATTN_EXT on the GPU; returns dst (B, Lq, H, Dv) float32.
 
     ``rope`` is a KdFaRope (rope_table / rope_axes) to rotate Q and K on load.
@@ -273,7 +289,7 @@ def flash_attn_ext(q, k, v, mask=None, scale=None, max_bias=0.0, logit_softcap=0
     if dst is None:
         dst = torch.empty(out_shape(q, v), dtype=torch.float32, device=q.device)
     d = make_desc(q, k, v, mask, dst, scale, max_bias, logit_softcap)
-    st = run_desc(d, rope, stream)
+    st = run_desc(d, rope, stream, workspace)
     if st != OK:
         raise KdFaError(st, "kd_fa_rope_run" if rope is not None else "kd_fa_run")
     return dst

@@ -172,3 +172,13 @@ def test_empty_query_is_a_no_op():
     d.q.data = 16        # zero rows: any aligned non-null pointer, never read
     d.dst.data = 16
     assert kd_fa.lib().kd_fa_run(ctypes.byref(d), None) == kd_fa.OK
+
+
+def test_workspace_size_and_null_workspace():
+    q, k, v, m, dst = _node(B=2, H=8, Lq=60, Lk=60, qt=torch.bfloat16, kt=torch.bfloat16, Hkv=2)
+    d = kd_fa.make_desc(q, k, v, None, dst, 0.1)
+    assert kd_fa.workspace_size(d) == 128 * 60 * 2 * 2 * 2
+    bad = kd_fa.make_desc(q[..., :64], k[..., :64], v[..., :64], None, dst[..., :64], 0.1)
+    assert kd_fa.workspace_size(bad) == 0
+    rope = kd_fa.rope_table(torch.zeros((60, 128)))
+    assert kd_fa.lib().kd_fa_rope_run_ws(ctypes.byref(d), ctypes.byref(rope), None, 0, None) == kd_fa.ERR_NULL

@@ -178,6 +178,41 @@ def test_rope_fused_equals_prerotated(dt):
     assert_parity(gather_rows(fused, np.arange(4 * L), 4, L), ref, "rope fused")
 
 
+@pytest.mark.parametrize("mode", ["table", "axes"])
+def test_rope_workspace_equals_fused(mode):
+    """kd_fa_rope_run_ws (K rotated once into a workspace) == kd_fa_rope_run,
+    bitwise, with GQA, batch broadcast, strided K and a partial last tile."""
+    _need_gpu()
+    _announce(f"rope workspace vs fused ({mode})")
+    T, Hp, Wp = 3, 5, 7
+    L = T * Hp * Wp                     # 105 tokens: partial 64-key tile
+    B, H, Hkv = 2, 4, 2
+    q, k, v = qkv(B, H, L, L, torch.bfloat16, seed=51, Hkv=Hkv, Bk=1, q_dtype=torch.float32)
+    qg, vg = _gpu(q, v)
+    kbig = torch.zeros((1, Hkv, L, D + 8), dtype=torch.bfloat16)
+    kbig[..., :D] = k
+    kg = kbig.to(DEV)[..., :D]          # 272-byte rows
+    if mode == "table":
+        tab = torch.from_numpy(kd_fa.visual_rope_table(T, Hp, Wp, AXES, SCALE_FACTOR, THETA)).to(DEV)
+        rope = kd_fa.rope_table(tab)
+    else:
+        ax = torch.from_numpy(kd_fa.axes_rope_table(T, Hp, Wp, AXES, SCALE_FACTOR, THETA)).to(DEV)
+        rope = kd_fa.rope_axes(ax, (T, Hp, Wp), AXES)
+    fused = _run(qg, kg, vg, rope=rope).clone()
+    d = kd_fa.make_desc(qg, kg, vg, None, torch.empty_like(fused), 1.0 / D ** 0.5)
+    nbytes = kd_fa.workspace_size(d)
+    assert nbytes == 128 * L * Hkv * 1 * 2
+    ws = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=DEV)
+    out = kd_fa.flash_attn_ext(qg, kg, vg, rope=rope, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(out, fused)
+    # the workspace holds the rotated K: equal to the oracle's rotation
+    table = kd_fa.visual_rope_table(T, Hp, Wp, AXES, SCALE_FACTOR, THETA)
+    assert torch.equal(ws.view(1, Hkv, L, D).cpu(), _rot(k, table, torch.bfloat16))
+    small = torch.empty(nbytes // 2 - 8, dtype=torch.bfloat16, device=DEV)
+    assert kd_fa.run_desc(d, rope, None, small) == kd_fa.ERR_LAYOUT
+
+
 def test_rope_axes_equals_table():
     _need_gpu()
     _announce("rope axes vs table")
