@@ -288,3 +288,37 @@ def test_self_attention_production_sampled(cfg):
     ref = orc.fa_f64(q.cpu(), k.cpu(), v.cpu(), rope=orc.rope_table(tab_c), rows=rows)
     m = assert_parity(gather_rows(out, rows, HEADS, L), ref, name)
     print(f"[{name}] {m}", flush=True)
+
+
+def test_cpp_ops_attention_mirror_on_gpu(tmp_path):
+    """kd::attention (C++ mirror of ops::attention) on the reference's
+    activation layout q [C, Lq, N] F32, k/v [C, Lk, N] bf16, with the RoPE
+    table, run by the compiled driver kandinsky.cpp_amd/kd_attention_run."""
+    import os
+    import subprocess
+    _need_gpu()
+    exe = os.path.join(os.path.dirname(kd_fa.LIB_PATH), "kd_attention_run")
+    if not os.path.exists(exe):
+        pytest.fail("kd_attention_run is not built (make -C kandinsky.cpp_amd)")
+    _announce("C++ ops::attention mirror")
+    N, H, T, Hp, Wp = 2, 4, 2, 6, 8
+    L = T * Hp * Wp
+    g = torch.Generator().manual_seed(61)
+    qa = torch.randn((N, L, H * D), generator=g)                      # F32 activations
+    ka = torch.randn((N, L, H * D), generator=g).to(torch.bfloat16)
+    va = torch.randn((N, L, H * D), generator=g).to(torch.bfloat16)
+    table = kd_fa.visual_rope_table(T, Hp, Wp, AXES, SCALE_FACTOR, THETA)
+    files = {n: str(tmp_path / f"{n}.bin") for n in ("q", "k", "v", "o", "r")}
+    qa.numpy().tofile(files["q"])
+    ka.view(torch.int16).numpy().tofile(files["k"])
+    va.view(torch.int16).numpy().tofile(files["v"])
+    table.tofile(files["r"])
+    res = subprocess.run([exe, str(H), str(L), str(L), str(N), "bf16", files["q"], files["k"],
+                          files["v"], files["o"], files["r"]], capture_output=True, text=True, timeout=60)
+    assert res.returncode == 0, res.stderr
+    out = torch.from_numpy(np.fromfile(files["o"], dtype=np.float32).reshape(N, L, H, D))
+    q4 = qa.view(N, L, H, D).permute(0, 2, 1, 3).contiguous()
+    k4 = ka.view(N, L, H, D).permute(0, 2, 1, 3).contiguous()
+    v4 = va.view(N, L, H, D).permute(0, 2, 1, 3).contiguous()
+    ref = orc.fa_f64(q4, k4, v4, rope=orc.rope_table(torch.from_numpy(table)))
+    assert_parity(gather_rows(out, np.arange(N * H * L), H, L), ref, "C++ mirror")
