@@ -14,11 +14,7 @@
 // the previous tile is being computed.  With RoPE, K instead passes through
 // registers, where it is rotated on its way into LDS.
 //
-// Operand layouts of v_mfma_f32_32x32x16 (wave64):
-//   A (32 x 16): lane l holds row l%32, k = (l/32)*8 .. +7
-//   B (16 x 32): lane l holds column l%32, k = (l/32)*8 .. +7
-//   C (32 x 32): lane l, element i holds row 8*(i/4) + 4*(l/32) + i%4,
-//                column l%32
+// (MFMA operand layouts: kd_fa_device.h.)
 // S^T uses A = K (keys on M) and B = Q^T (queries on N): each lane holds 16
 // scores of one query per 32-key block.  The K rows of each 32-key block sit
 // in LDS with bits 2 and 3 of the key index exchanged, which makes score
@@ -31,207 +27,60 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "kd_fa_kernel.h"
+#include "kd_fa_device.h"
 
 namespace kdfa {
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-
-#define LDS_PTR(T, p) ((__attribute__((address_space(3))) T *)(p))
-// LDS addresses are handled as 32-bit address-space-3 pointers throughout
-// (generic pointers would cost two registers each)
-typedef __attribute__((address_space(3))) char lds_t;
-
-constexpr int kD = 128;          // head dim (Dk = Dv)
 constexpr int kWaves = KD_FA_WAVES;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBM = 32 * kWaves; // query rows per workgroup
-constexpr int kBN = 64;          // keys per tile
-constexpr int kTileBytes = kBN * kD * 2;   // one K or V tile
-constexpr int kRounds = kTileBytes / (kThreads * 16);  // 16-byte loads per thread per tile
-constexpr float kLog2e = 1.4426950408889634f;
-// Lazy rescale: the running max moves only when a row max exceeds it by
-// more than kTau (log2 units), so P <= 2^kTau before normalisation.
-constexpr float kTau = 8.0f;
-// Unmasked path: a row's weights against the running max may grow up to
-// this sum before the max is refreshed (2^64: no F32 overflow of O for any
-// |V| < 2^40 and Lk < 2^20).
-constexpr float kSumCap = 18446744073709551616.0f;
+
+constexpr int kBN = 64;                             // keys per tile
+constexpr int kTileBytes = kBN * kD * 2;            // one K or V tile
+constexpr int kRounds = kTileBytes / (kThreads * 16);  // 16-byte DMA rounds per thread per tile
 
 static_assert(kBM == kBlockM, "block rows");
+static_assert(kRounds * kThreads * 16 == kTileBytes, "tile shape");
+
+template <bool B> struct BC { static constexpr bool value = B; };
+
+// Instruction order of one S^T product for the scheduler: PRE pairs of K
+// fragment reads ahead, then per k-step two MFMAs and the next pair of reads.
+// (sched_group_barrier masks: 0x008 MFMA, 0x100 DS read.)
+template <int KS, int PRE> __device__ __forceinline__ void sched_qk_step() {
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    if constexpr (KS + PRE < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+}
+template <int PRE> __device__ __forceinline__ void sched_qk() {
+    for (int i = 0; i < PRE; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    sched_qk_step<0, PRE>(); sched_qk_step<1, PRE>(); sched_qk_step<2, PRE>(); sched_qk_step<3, PRE>();
+    sched_qk_step<4, PRE>(); sched_qk_step<5, PRE>(); sched_qk_step<6, PRE>(); sched_qk_step<7, PRE>();
+}
 
 // Wave priority around the MFMA sections (tuning switch).
 #ifndef KD_FA_SETPRIO
 #define KD_FA_SETPRIO 0
+#endif
+// K-fragment prefetch distance (k-steps) and the explicit DS-read / MFMA
+// interleave of S^T = K Q^T (for the kernels that rotate K tiles on load,
+// which hold more registers, separately)
+#ifndef KD_FA_KPRE
+#define KD_FA_KPRE 2
+#endif
+#ifndef KD_FA_SCHED
+#define KD_FA_SCHED 1
+#endif
+#ifndef KD_FA_KPRE_KR
+#define KD_FA_KPRE_KR 0
+#endif
+#ifndef KD_FA_SCHED_KR
+#define KD_FA_SCHED_KR 0
 #endif
 #if KD_FA_SETPRIO
 #define KD_FA_PRIO(x) __builtin_amdgcn_s_setprio(x)
 #else
 #define KD_FA_PRIO(x) ((void)0)
 #endif
-
-// ---------------------------------------------------------------------
-// element-type traits: MFMA and F32 <-> storage conversions
-// ---------------------------------------------------------------------
-template <typename T> struct Elem;
-
-template <> struct Elem<__bf16> {
-    typedef bf16x8 vec8;
-    static __device__ __forceinline__ f32x16 mfma(vec8 a, vec8 b, f32x16 c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-    }
-    static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-        bf16x2 v = __builtin_convertvector((f32x4){lo, hi, 0.f, 0.f}.xy, bf16x2);
-        return __builtin_bit_cast(uint32_t, v);
-    }
-    static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
-    static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-    // acc + lo(w) + hi(w), exact products by 1.0 (v_dot2c_f32_bf16)
-    static __device__ __forceinline__ float sum2(uint32_t w, float acc) {
-        const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one, acc, false);
-    }
-};
-
-template <> struct Elem<_Float16> {
-    typedef f16x8 vec8;
-    static __device__ __forceinline__ f32x16 mfma(vec8 a, vec8 b, f32x16 c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-    }
-    static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-        f16x2 v = __builtin_convertvector((f32x4){lo, hi, 0.f, 0.f}.xy, f16x2);
-        return __builtin_bit_cast(uint32_t, v);
-    }
-    static __device__ __forceinline__ float lo(uint32_t w) { return (float)__builtin_bit_cast(f16x2, w).x; }
-    static __device__ __forceinline__ float hi(uint32_t w) { return (float)__builtin_bit_cast(f16x2, w).y; }
-    static __device__ __forceinline__ float sum2(uint32_t w, float acc) {
-        const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
-        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, acc, false);
-    }
-};
-
-static __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
-static __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-static __device__ __forceinline__ float f16_lo(uint32_t w) { return (float)__builtin_bit_cast(f16x2, w).x; }
-static __device__ __forceinline__ float f16_hi(uint32_t w) { return (float)__builtin_bit_cast(f16x2, w).y; }
-
-static __device__ __forceinline__ u32x4 ld16(const void *p) { return *reinterpret_cast<const u32x4 *>(p); }
-
-// Eight consecutive elements of a row (16-byte aligned) as F32.
-static __device__ __forceinline__ void load8_f32(const char *p, int type, float x[8]) {
-    if (type == KD_FA_TYPE_F32) {
-        const f32x4 a = *reinterpret_cast<const f32x4 *>(p);
-        const f32x4 b = *reinterpret_cast<const f32x4 *>(p + 16);
-        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-    } else {
-        const u32x4 w = ld16(p);
-        if (type == KD_FA_TYPE_BF16) {
-            for (int j = 0; j < 4; ++j) { x[2 * j] = bf16_lo(w[j]); x[2 * j + 1] = bf16_hi(w[j]); }
-        } else {
-            for (int j = 0; j < 4; ++j) { x[2 * j] = f16_lo(w[j]); x[2 * j + 1] = f16_hi(w[j]); }
-        }
-    }
-}
-
-// n / d for 0 <= n < 2^24, d >= 1, given rd = 1.0f / d: the float quotient
-// is within one of the true one, and one correction step each way fixes it.
-static __device__ __forceinline__ int div_small(int n, int d, float rd) {
-    int q = (int)((float)n * rd);
-    const int r = n - q * d;
-    q += (r >= d) - (r < 0);
-    return q;
-}
-
-// (cos, sin) pairs for columns d0 .. d0+7 of token `tok`: TABLE reads row
-// `tok` of the [D, L] table; AXES reads the row of the token's t, h or w
-// coordinate from the per-axis table holding that column block.
-template <int RM>
-static __device__ __forceinline__ const float *rope_ptr(const Args &a, int tok, int d0) {
-    if (RM == KD_FA_ROPE_TABLE)
-        return reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.rope_tab) +
-                                               (int64_t)tok * a.rope_nb1) + d0;
-    const int tw = div_small(tok, a.grid_w, a.rcp_w);          // t*Hp + h
-    if (d0 < a.axis0) return a.axes + div_small(tw, a.grid_h, a.rcp_h) * a.axis0 + d0;
-    if (d0 < a.axis0 + a.axis1) {
-        const int h = tw - div_small(tw, a.grid_h, a.rcp_h) * a.grid_h;
-        return a.axes + a.grid_t * a.axis0 + h * a.axis1 + (d0 - a.axis0);
-    }
-    const int w = tok - tw * a.grid_w;
-    return a.axes + a.grid_t * a.axis0 + a.grid_h * a.axis1 + w * a.axis2 + (d0 - a.axis0 - a.axis1);
-}
-
-// rope::apply's pair rotation (src/rope.hpp:137-138): every product and
-// every sum rounded to F32 on its own, as the separate ggml ops do.
-static __device__ __forceinline__ void rotate8(float x[8], f32x4 c0, f32x4 c1) {
-#pragma clang fp contract(off)
-    const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-    for (int j = 0; j < 4; ++j) {
-        const float x0 = x[2 * j], x1 = x[2 * j + 1];
-        const float c = cs[2 * j], s = cs[2 * j + 1];
-        const float p0 = x0 * c, p1 = x1 * s, p2 = x0 * s, p3 = x1 * c;
-        x[2 * j] = p0 - p1;
-        x[2 * j + 1] = p2 + p3;
-    }
-}
-
-// K tile: LDS row r holds key k_row_of(r) (bits 2 and 3 exchanged, its own
-// inverse); 16-byte chunk c of a row is stored at c ^ (r & 15).
-// V tile: row r holds key r; chunk c is stored at c ^ v_swz(r).  Both keep
-// the MFMA operand reads free of bank conflicts on 32- and 64-bank LDS.
-static __device__ __forceinline__ int k_row_of(int key) {
-    return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
-}
-static __device__ __forceinline__ int v_swz(int r) { return ((r & 3) << 2) | (r & 2); }
-
-// One wave-wide 16-byte-per-lane DMA: global (base + lane offset) -> LDS
-// (wave-uniform destination + 16 * lane).  Written as the instruction itself
-// so that the uniform base stays in SGPRs with a 32-bit lane offset (no
-// per-lane 64-bit address registers); the compiler does not track it, so
-// every consumer waits with an explicit s_waitcnt vmcnt(0) + barrier.
-static __device__ __forceinline__ void dma16(const char *base, uint32_t lane_off, lds_t *lds_wave_base) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_wave_base);
-    asm volatile("global_load_lds_dwordx4 %0, %1" :: "v"(lane_off), "s"(base), "{m0}"(m0));
-}
-
-// v_max3_f32 directly: the maxnum builtins would first canonicalise every
-// input (one extra v_max_f32 each) to quiet signalling NaNs, which the
-// scores never are
-static __device__ __forceinline__ float max3(float a, float b, float c) {
-    float d;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-    return d;
-}
-
-// max of 32 values: two interleaved chains of v_max3_f32
-static __device__ __forceinline__ float max32(const float *p) {
-    float x = max3(p[0], p[1], p[2]);
-    float y = max3(p[3], p[4], p[5]);
-#pragma unroll
-    for (int i = 6; i < 30; i += 4) {
-        x = max3(x, p[i], p[i + 1]);
-        y = max3(y, p[i + 2], p[i + 3]);
-    }
-    return max3(x, y, __builtin_fmaxf(p[30], p[31]));
-}
-
-// max over the lane pair (l, l ^ 32) that shares one query row
-static __device__ __forceinline__ float pair_max(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-static __device__ __forceinline__ float pair_sum(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
 
 template <typename T, bool HAS_MASK, int RM, bool KROPE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
@@ -322,11 +171,14 @@ void fa_fwd_d128(Args a) {
         v_dma[j] = (uint32_t)r * (uint32_t)a.v_nb1 + ((dma_pc ^ v_swz(r)) << 4);
         k_dma[j] = (uint32_t)k_row_of(r) * (uint32_t)a.k_nb1 + ((dma_pc ^ (r & 15)) << 4);
     }
-    auto issue_v = [&](int t, lds_t *dV) {
+    auto issue_v = [&](int t, lds_t *dV) __attribute__((always_inline)) {
         const char *vt = vbase + (int64_t)t * kBN * a.v_nb1;
         if ((t + 1) * kBN <= Lk) {
+            // round j covers rows 4*kWaves*j + (row of round 0): only the
+            // uniform base moves
 #pragma unroll
-            for (int j = 0; j < kRounds; ++j) dma16(vt, v_dma[j], dV + (wave + kWaves * j) * 1024);
+            for (int j = 0; j < kRounds; ++j)
+                dma16(vt + (int64_t)j * 4 * kWaves * a.v_nb1, v_dma[0], dV + (wave + kWaves * j) * 1024);
         } else {
 #pragma unroll
             for (int j = 0; j < kRounds; ++j) {
@@ -337,11 +189,12 @@ void fa_fwd_d128(Args a) {
             }
         }
     };
-    auto issue_k = [&](int t, lds_t *dK) {   // K without RoPE
+    auto issue_k = [&](int t, lds_t *dK) __attribute__((always_inline)) {   // K without RoPE
         const char *kt = kbase + (int64_t)t * kBN * a.k_nb1;
         if ((t + 1) * kBN <= Lk) {
 #pragma unroll
-            for (int j = 0; j < kRounds; ++j) dma16(kt, k_dma[j], dK + (wave + kWaves * j) * 1024);
+            for (int j = 0; j < kRounds; ++j)
+                dma16(kt + (int64_t)j * 4 * kWaves * a.k_nb1, k_dma[0], dK + (wave + kWaves * j) * 1024);
         } else {
 #pragma unroll
             for (int j = 0; j < kRounds; ++j) {
@@ -352,7 +205,7 @@ void fa_fwd_d128(Args a) {
             }
         }
     };
-    auto issue_tile = [&](int t, lds_t *dK, lds_t *dV) {
+    auto issue_tile = [&](int t, lds_t *dK, lds_t *dV) __attribute__((always_inline)) {
         issue_v(t, dV);
         if (!KR) issue_k(t, dK);
     };
@@ -367,7 +220,7 @@ void fa_fwd_d128(Args a) {
         const int r = 4 * (wave + kWaves * j) + dma_row;
         tab_off[j] = (uint32_t)k_row_of(r) * (uint32_t)a.rope_nb1 + (((dma_pc ^ (r & 15)) << 5));
     }
-    auto rope_load = [&](int t) {
+    auto rope_load = [&](int t) __attribute__((always_inline)) {
         const char *kt = kbase + (int64_t)t * kBN * a.k_nb1;
         const bool full = (t + 1) * kBN <= Lk;
 #pragma unroll
@@ -391,7 +244,7 @@ void fa_fwd_d128(Args a) {
             }
         }
     };
-    auto rope_store = [&](lds_t *dK) {
+    auto rope_store = [&](lds_t *dK) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < kRounds; ++j) {
             const int u = tid + kThreads * j;
@@ -407,7 +260,7 @@ void fa_fwd_d128(Args a) {
     // mask values of this lane's 32 keys (key 16*hh + 8*hi + e of 32-key
     // block mb at index mb*16 + hh*8 + e), prefetched one tile ahead
     u32x4 mraw[4];
-    auto mask_load = [&](int t) {
+    auto mask_load = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
@@ -442,20 +295,33 @@ void fa_fwd_d128(Args a) {
         v_rd[dblk] = 2048 * hi + 256 * v_sub + (((4 * dblk + v_c_lo) ^ v_swz(v_sub)) << 4) + 8 * (lane & 1);
 
     // ---- S^T = K Q^T for one 64-key tile ---------------------------------------
-    auto qk = [&](const lds_t *ks_, f32x16 &s0, f32x16 &s1) {
+    // K fragments are read kKPre k-steps ahead of the MFMAs that use them,
+    // so that LDS latency overlaps the products instead of stalling each
+    // pair of them
+    auto qk = [&](const lds_t *ks_, f32x16 &s0, f32x16 &s1) __attribute__((always_inline)) {
+        constexpr int kKPre = KR ? KD_FA_KPRE_KR : KD_FA_KPRE;
         s0 = (f32x16){};
         s1 = (f32x16){};
+        vec8 ka[8][2];
+#pragma unroll
+        for (int ks = 0; ks < kKPre; ++ks) {
+            ka[ks][0] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks]);
+            ka[ks][1] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks] + 32 * 256);
+        }
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
-            const vec8 a0 = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks]);
-            const vec8 a1 = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks] + 32 * 256);
-            s0 = E::mfma(a0, qf[ks], s0);
-            s1 = E::mfma(a1, qf[ks], s1);
+            if (ks + kKPre < 8) {
+                ka[ks + kKPre][0] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks + kKPre]);
+                ka[ks + kKPre][1] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks + kKPre] + 32 * 256);
+            }
+            s0 = E::mfma(ka[ks][0], qf[ks], s0);
+            s1 = E::mfma(ka[ks][1], qf[ks], s1);
         }
+        if constexpr (KR ? KD_FA_SCHED_KR : KD_FA_SCHED) sched_qk<kKPre>();
     };
 
     // rescale O and the sums when the running max moves by more than kTau
-    auto update_max = [&](float mx) {
+    auto update_max = [&](float mx) __attribute__((always_inline)) {
         if (__builtin_amdgcn_ballot_w64(mx > m_run + kTau) != 0) {
             const float m_new = __builtin_fmaxf(m_run, mx);
             const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -483,11 +349,11 @@ void fa_fwd_d128(Args a) {
         }
         return sum;
     };
-    auto pack_p = [&](const float *p, vec8 pb[4]) { l_half += pack_sum(p, pb); };
+    auto pack_p = [&](const float *p, vec8 pb[4]) __attribute__((always_inline)) { l_half += pack_sum(p, pb); };
 
     // online softmax with the additive mask: logits s*c2 + mask*log2(e);
     // -inf mask entries (and keys past Lk, filled with -inf) stay -inf
-    auto softmax_masked = [&](const f32x16 &s0, const f32x16 &s1, const float *mv, vec8 pb[4]) {
+    auto softmax_masked = [&](const f32x16 &s0, const f32x16 &s1, const float *mv, vec8 pb[4]) __attribute__((always_inline)) {
         float p[32];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -505,7 +371,7 @@ void fa_fwd_d128(Args a) {
     };
 
     // ---- O^T += V^T P^T ------------------------------------------------------
-    auto pv = [&](const lds_t *vs_, const vec8 pb[4]) {
+    auto pv = [&](const lds_t *vs_, const vec8 pb[4]) __attribute__((always_inline)) {
 #pragma unroll
         for (int kst = 0; kst < 4; ++kst) {
 #pragma unroll
@@ -519,7 +385,7 @@ void fa_fwd_d128(Args a) {
         }
     };
 
-    auto load_tile_sync = [&](int t, lds_t *dK, lds_t *dV) {
+    auto load_tile_sync = [&](int t, lds_t *dK, lds_t *dV) __attribute__((always_inline)) {
         issue_tile(t, dK, dV);
         if (KR) {
             rope_load(t);
@@ -529,18 +395,67 @@ void fa_fwd_d128(Args a) {
 
     const int n_tiles = (Lk + kBN - 1) / kBN;
 
+    // Unmasked softmax of one 64-key step (scores s0, s1 of keys key0 ..
+    // key0+63) and O^T += V^T P^T with the V rows at vs_.  The running max
+    // m_run is not refreshed every step: the exponents are taken against the
+    // current m_run, and only when a row's sum of weights leaves
+    // [0, 2^kSumCap] (a score far above m_run, or the first step with
+    // m_run = -inf) is the step's exact row max computed, O rescaled and the
+    // exponents redone.  Weights stay <= 2^kSumCap, far inside the F32 /
+    // bf16 range.  TAIL: keys past Lk (last tile only) read clamped K rows,
+    // i.e. copies of key Lk-1 -- finite scores that never raise the row
+    // max; their weights are zeroed after the exponent.
+    auto soft_pv = [&](auto tail_c, int key0, const f32x16 &s0, const f32x16 &s1, const lds_t *vs_) __attribute__((always_inline)) {
+        constexpr bool TAIL = decltype(tail_c)::value;
+        auto drop_tail = [&](float *p) __attribute__((always_inline)) {
+            if (TAIL) {
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    const int key = key0 + (i >> 4) * 32 + 16 * ((i >> 3) & 1) + 8 * hi + (i & 7);
+                    p[i] = key < Lk ? p[i] : 0.0f;
+                }
+            }
+        };
+        vec8 pb[4];
+        float p[32];
+        float nm = -m_run;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], c2, nm));
+            p[16 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], c2, nm));
+        }
+        drop_tail(p);
+        float sum = pack_sum(p, pb);
+        const float pair = pair_sum(sum);
+        // !(x <= cap) also catches NaN (inf - inf with m_run = -inf)
+        if (__builtin_amdgcn_ballot_w64(!(pair <= kSumCap)) != 0) {
+            float q[32];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) { q[i] = s0[i]; q[16 + i] = s1[i]; }
+            update_max(pair_max(max32(q)) * c2);
+            nm = -m_run;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], c2, nm));
+                p[16 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], c2, nm));
+            }
+            drop_tail(p);
+            sum = pack_sum(p, pb);
+        }
+        l_half += sum;
+        KD_FA_PRIO(1);
+        pv(vs_, pb);
+        KD_FA_PRIO(0);
+    };
+
     if constexpr (!HAS_MASK) {
         // Two LDS stages; tile t+1 streams in while tile t is computed.
-        // The running max m_run is not refreshed every tile: the exponents
-        // of tile t are taken against the current m_run, and only when a
-        // row's sum of weights leaves [0, 2^kSumCap] (a score far above
-        // m_run, or the first tile with m_run = -inf) is the tile's exact
-        // row max computed, O rescaled and the exponents redone.  Weights
-        // stay <= 2^kSumCap, far inside the F32 / bf16 range.
         if (n_tiles > 0) load_tile_sync(0, sK0, sV0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        auto step = [&](int t, const lds_t *ks_, const lds_t *vs_, lds_t *nK, lds_t *nV) {
+        // TAIL: the last, partial tile (a compile-time variant, so that full
+        // tiles carry no branch around the weights)
+        auto step = [&](auto tail_c, int t, const lds_t *ks_, const lds_t *vs_, lds_t *nK, lds_t *nV) __attribute__((always_inline)) {
             const bool has_next = t + 1 < n_tiles;
             if (has_next) {
                 issue_tile(t + 1, nK, nV);
@@ -550,56 +465,21 @@ void fa_fwd_d128(Args a) {
             KD_FA_PRIO(1);
             qk(ks_, s0, s1);
             KD_FA_PRIO(0);
-            // keys past Lk (last tile only) read clamped K rows, i.e. copies
-            // of key Lk-1: finite scores that never raise the row max; their
-            // weights are zeroed after the exponent
-            const bool tail = (t + 1) * kBN > Lk;
-            auto drop_tail = [&](float *p) {
-                if (tail) {
-#pragma unroll
-                    for (int i = 0; i < 32; ++i) {
-                        const int key = t * kBN + (i >> 4) * 32 + 16 * ((i >> 3) & 1) + 8 * hi + (i & 7);
-                        p[i] = key < Lk ? p[i] : 0.0f;
-                    }
-                }
-            };
-            vec8 pb[4];
-            float p[32];
-            float nm = -m_run;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], c2, nm));
-                p[16 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], c2, nm));
-            }
-            drop_tail(p);
-            float sum = pack_sum(p, pb);
-            const float pair = pair_sum(sum);
-            // !(x <= cap) also catches NaN (inf - inf with m_run = -inf)
-            if (__builtin_amdgcn_ballot_w64(!(pair <= kSumCap)) != 0) {
-                float q[32];
-#pragma unroll
-                for (int i = 0; i < 16; ++i) { q[i] = s0[i]; q[16 + i] = s1[i]; }
-                update_max(pair_max(max32(q)) * c2);
-                nm = -m_run;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], c2, nm));
-                    p[16 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], c2, nm));
-                }
-                drop_tail(p);
-                sum = pack_sum(p, pb);
-            }
-            l_half += sum;
-            KD_FA_PRIO(1);
-            pv(vs_, pb);
-            KD_FA_PRIO(0);
+            soft_pv(tail_c, t * kBN, s0, s1, vs_);
             if (KR && has_next) rope_store(nK);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
         };
-        for (int t = 0; t < n_tiles; t += 2) {
-            step(t, sK0, sV0, sK1, sV1);
-            if (t + 1 < n_tiles) step(t + 1, sK1, sV1, sK0, sV0);
+        const int n_full = Lk / kBN;
+        for (int t = 0; t < n_full; t += 2) {
+            step(BC<false>(), t, sK0, sV0, sK1, sV1);
+            if (t + 1 < n_full) step(BC<false>(), t + 1, sK1, sV1, sK0, sV0);
+        }
+        if (n_full < n_tiles) {
+            if (n_full & 1)
+                step(BC<true>(), n_full, sK1, sV1, sK0, sV0);
+            else
+                step(BC<true>(), n_full, sK0, sV0, sK1, sV1);
         }
     } else {
         // masked: two LDS stages; a tile whose mask is -inf for all of this
@@ -610,7 +490,7 @@ void fa_fwd_d128(Args a) {
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        auto mstep = [&](int t, const lds_t *ks_, const lds_t *vs_, lds_t *nK, lds_t *nV) {
+        auto mstep = [&](int t, const lds_t *ks_, const lds_t *vs_, lds_t *nK, lds_t *nV) __attribute__((always_inline)) {
             const bool has_next = t + 1 < n_tiles;
             if (has_next) {
                 issue_tile(t + 1, nK, nV);
