@@ -174,6 +174,10 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, void *ws, size_t ws_bytes, voi
     }
     a.n_qt = (int32_t)((Lq + kdfa::kBlockM - 1) / kdfa::kBlockM);
     a.n_blocks = (int32_t)(a.n_qt * H * B);
+    // a mask row block shared by every head is read once per q-tile when the
+    // heads of a q-tile run back to back (K and V of all heads then share the
+    // L2 instead, which the short text keys of the cross-attention allow)
+    a.heads_inner = (a.m && d->mask.ne[2] == 1 && H > 1 && d->k.ne[1] <= 1024) ? 1 : 0;
 
     hipStream_t hs = static_cast<hipStream_t>(stream);
     bool k_rope = rope_on;

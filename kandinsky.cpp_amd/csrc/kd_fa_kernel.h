@@ -38,6 +38,7 @@ struct Args {
     float rcp_h, rcp_w;   // 1.0f / grid_h, 1.0f / grid_w
     int32_t n_qt;       // query tiles per (b, h)
     int32_t n_blocks;   // n_qt * H * B
+    int32_t heads_inner;  // block order: heads fastest (mask shared by all heads)
 };
 
 // Enqueue the forward kernel for K/V element type kv_type on `stream`.

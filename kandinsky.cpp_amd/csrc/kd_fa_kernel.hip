@@ -110,10 +110,21 @@ void fa_fwd_d128(Args a) {
     const int pid = blockIdx.x;
     const int per = a.n_blocks >> 3;
     const int lid = pid < per * 8 ? (pid & 7) * per + (pid >> 3) : pid;
-    const int qt = lid % a.n_qt;
-    const int bh = lid / a.n_qt;
-    const int h = bh % a.H;
-    const int b = bh / a.H;
+    // Logical order: the q-tiles of one head in a row (they share K and V),
+    // or, for a mask shared by all heads, the heads of one q-tile in a row
+    // (they share the mask tile).
+    int qt, h, b;
+    if (a.heads_inner) {
+        h = lid % a.H;
+        const int r = lid / a.H;
+        qt = r % a.n_qt;
+        b = r / a.n_qt;
+    } else {
+        qt = lid % a.n_qt;
+        const int bh = lid / a.n_qt;
+        h = bh % a.H;
+        b = bh / a.H;
+    }
 
     const char *kbase = a.k + (int64_t)(h / a.rk2) * a.k_nb2 + (int64_t)(b / a.rk3) * a.k_nb3;
     const char *vbase = a.v + (int64_t)(h / a.rv2) * a.v_nb2 + (int64_t)(b / a.rv3) * a.v_nb3;
