@@ -185,6 +185,15 @@ def main():
         ms_n = time_launches(torch, lambda: kd_fa.run_desc(desc, None, stream), args.steps, args.warmup, stream)
         sec["self_attn_norope_ms"] = round(ms_n, 4)
         sec["self_attn_norope_tflops"] = round(flop / (ms_n * 1e-3) / 1e12, 2)
+        # the DiT attention from the projections on (kd_fa_dit_run): query/key
+        # RMSNorm, RoPE, attention, K through the workspace
+        wq = rand(torch, (D,), 7, dev, torch.float32) * 0.3 + 1.0
+        wk = rand(torch, (D,), 8, dev, torch.float32) * 0.3 + 1.0
+        norm = kd_fa.qk_norm(wq, wk, 1e-6)
+        ms_d = time_launches(torch, lambda: kd_fa.run_desc(desc, rope, stream, ws, norm), args.steps, args.warmup,
+                             stream)
+        sec["self_attn_norm_rope_ws_ms"] = round(ms_d, 4)
+        sec["self_attn_norm_rope_ws_tflops"] = round(flop / (ms_d * 1e-3) / 1e12, 2)
         # text cross-attention: Q 31,744 x K/V 256, batch 2, padding mask 120 / 40 valid keys
         k2 = rand(torch, (B, HEADS, 256, D), 1002, dev, bf)
         v2 = rand(torch, (B, HEADS, 256, D), 2002, dev, bf)
@@ -198,6 +207,14 @@ def main():
         sec["cross_attn_ms"] = round(ms2, 4)
         sec["cross_attn_GBps"] = round(bytes2 / (ms2 * 1e-3) / 1e9, 1)
         sec["cross_attn_hbm_frac"] = round(bytes2 / (ms2 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
+        # the same with query/key RMSNorm and O stored as bf16 for out_layer
+        out2b = torch.empty((B, L, HEADS, D), device=dev, dtype=torch.bfloat16)
+        ws2 = torch.empty(k2.numel(), dtype=k2.dtype, device=dev)
+        d2b = kd_fa.make_desc(q, k2, v2, m2, out2b, 1.0 / D ** 0.5)
+        ms2b = time_launches(torch, lambda: kd_fa.run_desc(d2b, None, stream, ws2, norm), 20, 3, stream)
+        bytes2b = bytes2 - out2.numel() * 2
+        sec["cross_attn_norm_bf16out_ms"] = round(ms2b, 4)
+        sec["cross_attn_norm_bf16out_GBps"] = round(bytes2b / (ms2b * 1e-3) / 1e9, 1)
         # 60 x (self + cross) with fresh buffers per layer (3 rotating sets)
         sets = [(q, k, v)] + [tuple(rand(torch, (B, HEADS, L, D), 10 * s + j, dev, bf) for j in range(3))
                               for s in range(1, 3)]

@@ -25,7 +25,9 @@
  *   mask [Lk', Lq', Hm, Bm] F16, optional; Lk' >= Lk, Lq' >= Lq,
  *                           broadcast over heads (H % Hm == 0) and
  *                           batch (B % Bm == 0); row of query i is ne1 = i
- *   dst  [Dv, H, Lq, B]     F32, contiguous (ggml's permuted result)
+ *   dst  [Dv, H, Lq, B]     F32 (ggml's permuted result); or BF16 / F16,
+ *                           O rounded to nearest even on store -- the cast
+ *                           the reference's out_layer input takes, fused
  *   dst[b][i][h][:] = sum_j softmax_j(scale * <q_bhi, k_j> + mask[b,h,i,j]) v_j
  *   with h_kv = h / (H / Hkv) and b_kv = b / (B / Bk).  A row whose keys
  *   are all masked (-inf) is written as zeros.
@@ -65,7 +67,7 @@ enum {
     KD_FA_ERR_SHAPE      = -3,   /* shapes inconsistent with the op       */
     KD_FA_ERR_LAYOUT     = -4,   /* stride / alignment not supported      */
     KD_FA_ERR_PARAM      = -5,   /* max_bias, softcap or scale unsupported */
-    KD_FA_ERR_ROPE       = -6,   /* invalid RoPE descriptor               */
+    KD_FA_ERR_ROPE       = -6,   /* invalid RoPE or norm descriptor       */
     KD_FA_ERR_LAUNCH     = -7,   /* HIP launch failed                     */
     KD_FA_ERR_DEVICE     = -8    /* no gfx950 device / runtime error      */
 };
@@ -169,6 +171,45 @@ int kd_fa_rope_run_ws(const kd_fa_desc *desc, const kd_fa_rope *rope, void *work
 
 /* Bytes of K-sized workspace kd_fa_rope_run_ws needs (0 for an invalid node). */
 size_t kd_fa_rope_workspace_size(const kd_fa_desc *desc);
+
+/*
+ * RMSNorm of the Q and K head rows ahead of RoPE: the query_norm / key_norm
+ * modules of DiTSelfAttention and DiTCrossAttention
+ * (src/models/crossdit.hpp:135-136, 192-193; RMSNorm,
+ * src/core/module.hpp:163-180, computed by ops::rms_norm =
+ * ggml_rms_norm + ggml_mul, src/core/ops.hpp:76-80).  For a row x of Dk
+ * elements: mean = (float)(sum of the F32 squares, in double) / Dk, then
+ * x * (1.0f / sqrtf(mean + eps)) * weight, each product rounded to F32.
+ */
+typedef struct kd_fa_qk_norm {
+    const float *q_weight;   /* F32 [Dk] device pointer; NULL: Q not normalised */
+    const float *k_weight;   /* F32 [Dk] device pointer; NULL: K not normalised */
+    float        eps;        /* 1e-6 in the reference                            */
+} kd_fa_qk_norm;
+
+/*
+ * kd_fa_dit_run - the attention of DiTSelfAttention::forward and
+ * DiTCrossAttention::forward from the projections on
+ * (src/models/crossdit.hpp:134-150, 191-199): each head row of Q and K is
+ * normalised (norm != NULL, per weight given), then rotated (rope != NULL
+ * and mode != KD_FA_ROPE_NONE; the self-attention), then rounded to K's
+ * type and fed to the node.  The result is defined as kd_fa_run on
+ * q' = round_K(rot(rms(q) * wq)), k' = round_K(rot(rms(k) * wk)), with
+ * every step in F32 as kd_fa_qk_norm and kd_fa_rope_run state.
+ * workspace != NULL: K is transformed once into it (as kd_fa_rope_run_ws,
+ * same size rule; it holds k' afterwards); NULL: K tiles are transformed
+ * on load.  The two give bitwise equal results.  With a workspace K may be
+ * F32 -- the projection output, normalised and rotated before the one
+ * rounding to V's type, the reference's order (ops.hpp:167 casts after
+ * RoPE); kd_fa_dit_supports accepts an F32 K on that condition.
+ * norm == NULL and rope == NULL is kd_fa_run.
+ */
+int kd_fa_dit_run(const kd_fa_desc *desc, const kd_fa_rope *rope, const kd_fa_qk_norm *norm,
+                  void *workspace, size_t workspace_bytes, void *stream);
+
+/* kd_fa_rope_supports plus the checks of the norm descriptor.  Host-only. */
+int kd_fa_dit_supports(const kd_fa_desc *desc, const kd_fa_rope *rope,
+                       const kd_fa_qk_norm *norm, int *reason);
 
 /*
  * kd_fa_rope_supports - kd_fa_supports plus the checks of the RoPE

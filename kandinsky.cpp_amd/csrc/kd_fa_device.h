@@ -197,4 +197,62 @@ static __device__ __forceinline__ float pair_sum(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// ---------------------------------------------------------------------
+// RMSNorm of a head row (ops::rms_norm = ggml_rms_norm + ggml_mul,
+// src/core/ops.hpp:76-80): the squares rounded to F32 and summed in double,
+// mean = (float)(sum / 128), scale = 1.0f / sqrtf(mean + eps) (both
+// correctly rounded), then x * scale * w with each product rounded to F32.
+// A row's squares are spread over several lanes; the caller reduces the
+// partial double sums over them before rms_scale.
+// ---------------------------------------------------------------------
+static __device__ __forceinline__ double sum_sq8(const float x[8]) {
+#pragma clang fp contract(off)
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float sq = x[i] * x[i];
+        s += (double)sq;
+    }
+    return s;
+}
+
+// sqrtf as the C library computes it (correctly rounded): v_sqrt_f32 alone
+// is within 1 ulp only, so the root is taken in double -- whose square root
+// sequence is exact to well under a double ulp -- and rounded once; rounding
+// a square root from 53 to 24 bits cannot round twice (53 >= 2*24 + 2).
+static __device__ __forceinline__ float sqrt_rn(float x) { return (float)__builtin_sqrt((double)x); }
+
+static __device__ __forceinline__ float rms_scale(double sum, float eps) {
+    const float mean = (float)(sum * (1.0 / 128.0));
+    return 1.0f / sqrt_rn(mean + eps);
+}
+
+// x = x * scale * w[0..7] (two roundings per element)
+static __device__ __forceinline__ void rms_apply8(float x[8], float scale, f32x4 w0, f32x4 w1) {
+#pragma clang fp contract(off)
+    const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float y = x[i] * scale;
+        x[i] = y * w[i];
+    }
+}
+
+// sum of a double over the lane pair (l, l ^ 32)
+static __device__ __forceinline__ double pair_sum_f64(double x) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, x);
+    const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)u, (uint32_t)u, false, false);
+    const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(u >> 32), (uint32_t)(u >> 32), false, false);
+    const double a = __builtin_bit_cast(double, (uint64_t)lo[0] | ((uint64_t)hi[0] << 32));
+    const double b = __builtin_bit_cast(double, (uint64_t)lo[1] | ((uint64_t)hi[1] << 32));
+    return a + b;
+}
+
+// sum of a double over the 16 lanes of each aligned 16-lane group
+static __device__ __forceinline__ double sum16_f64(double x) {
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) x += __shfl_xor(x, m, 64);
+    return x;
+}
+
 }  // namespace kdfa

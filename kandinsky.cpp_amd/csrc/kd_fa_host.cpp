@@ -23,18 +23,23 @@ size_t elem_size(int type) { return type == KD_FA_TYPE_F32 ? 4 : 2; }
 bool is_16b(uint64_t x) { return (x & 15u) == 0; }
 bool is_16b(const void *p) { return is_16b(reinterpret_cast<uintptr_t>(p)); }
 
-// Conditions of kd_fa_supports.  `mask_vec` reports whether the mask rows
-// can be read 16 bytes at a time.
-int validate(const kd_fa_desc *d, const kd_fa_rope *r, bool *mask_vec) {
+// Conditions of kd_fa_supports (and of the RoPE and norm descriptors when
+// given).  `mask_vec` reports whether the mask rows can be read 16 bytes at
+// a time.
+// k_f32: an F32 K is accepted (kd_fa_dit_run with a workspace, where the K
+// pre-pass rounds it to V's type).
+int validate(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, bool *mask_vec,
+             bool k_f32 = false) {
     if (!d) return KD_FA_ERR_NULL;
     const kd_fa_tensor &q = d->q, &k = d->k, &v = d->v, &m = d->mask, &o = d->dst;
     if (!q.data || !k.data || !v.data || !o.data) return KD_FA_ERR_NULL;
 
     // types: Q is converted to K's type on load; K and V share one MFMA type
     if (q.type != KD_FA_TYPE_F32 && q.type != KD_FA_TYPE_F16 && q.type != KD_FA_TYPE_BF16) return KD_FA_ERR_TYPE;
-    if (k.type != KD_FA_TYPE_F16 && k.type != KD_FA_TYPE_BF16) return KD_FA_ERR_TYPE;
-    if (v.type != k.type) return KD_FA_ERR_TYPE;
-    if (o.type != KD_FA_TYPE_F32) return KD_FA_ERR_TYPE;
+    if (v.type != KD_FA_TYPE_F16 && v.type != KD_FA_TYPE_BF16) return KD_FA_ERR_TYPE;
+    if (k.type != v.type && !(k_f32 && k.type == KD_FA_TYPE_F32)) return KD_FA_ERR_TYPE;
+    // dst: the node's F32, or a 16-bit cast of it
+    if (o.type != KD_FA_TYPE_F32 && o.type != KD_FA_TYPE_F16 && o.type != KD_FA_TYPE_BF16) return KD_FA_ERR_TYPE;
     if (m.data && m.type != KD_FA_TYPE_F16) return KD_FA_ERR_TYPE;
 
     // op params: plain softmax attention only (ops.hpp:176 passes 0, 0)
@@ -95,6 +100,12 @@ int validate(const kd_fa_desc *d, const kd_fa_rope *r, bool *mask_vec) {
             return KD_FA_ERR_ROPE;
         }
     }
+
+    // RMSNorm weights: F32 [Dk], read 16 bytes at a time
+    if (n) {
+        if (!std::isfinite(n->eps) || n->eps < 0.0f) return KD_FA_ERR_ROPE;
+        if ((n->q_weight && !is_16b(n->q_weight)) || (n->k_weight && !is_16b(n->k_weight))) return KD_FA_ERR_LAYOUT;
+    }
     return KD_FA_OK;
 }
 
@@ -117,19 +128,24 @@ int device_ok() {
     return st == 1 ? KD_FA_OK : KD_FA_ERR_DEVICE;
 }
 
+// K-sized workspace in the attention's operand type (V's)
 size_t rope_ws_bytes(const kd_fa_desc *d) {
     return (size_t)kHeadDim * (size_t)d->k.ne[1] * (size_t)d->k.ne[2] * (size_t)d->k.ne[3] *
-           elem_size(d->k.type);
+           elem_size(d->v.type);
 }
 
-// ws != nullptr: rotate K once into ws (contiguous, K's type) and run the
-// attention with only Q rotated on load.
-int run(const kd_fa_desc *d, const kd_fa_rope *r, void *ws, size_t ws_bytes, void *stream) {
+// K is transformed (normalised and / or rotated) when a norm weight or a
+// RoPE mode asks for it: with ws != nullptr once into ws (contiguous, K's
+// type), after which the attention transforms only Q on load; without, by
+// the attention kernel on every K tile it loads.
+int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *ws, size_t ws_bytes,
+        void *stream) {
     bool mask_vec = false;
-    int st = validate(d, r, &mask_vec);
-    if (st != KD_FA_OK) return st;
     const bool rope_on = r && r->mode != KD_FA_ROPE_NONE;
-    if (ws && rope_on) {
+    const bool k_xform = rope_on || (n && n->k_weight);
+    int st = validate(d, r, n, &mask_vec, ws && k_xform);
+    if (st != KD_FA_OK) return st;
+    if (ws && k_xform) {
         if (!is_16b(ws) || ws_bytes < rope_ws_bytes(d)) return KD_FA_ERR_LAYOUT;
     }
     const int64_t Lq = d->q.ne[1], H = d->q.ne[2], B = d->q.ne[3];
@@ -152,6 +168,12 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, void *ws, size_t ws_bytes, voi
         a.m_ne2 = (int32_t)d->mask.ne[2]; a.m_ne3 = (int32_t)d->mask.ne[3];
     }
     a.o_nb1 = d->dst.nb[1]; a.o_nb2 = d->dst.nb[2]; a.o_nb3 = d->dst.nb[3];
+    a.o_type = d->dst.type;
+    if (n) {
+        a.qn_w = n->q_weight;
+        a.kn_w = n->k_weight;
+        a.norm_eps = n->eps;
+    }
     a.Lq = (int32_t)Lq;
     a.Lk = (int32_t)d->k.ne[1];
     a.H = (int32_t)H;
@@ -159,6 +181,7 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, void *ws, size_t ws_bytes, voi
     a.rk2 = (int32_t)(H / d->k.ne[2]); a.rk3 = (int32_t)(B / d->k.ne[3]);
     a.rv2 = (int32_t)(H / d->v.ne[2]); a.rv3 = (int32_t)(B / d->v.ne[3]);
     a.q_type = d->q.type;
+    a.k_type = d->k.type;
     a.mask_vec = mask_vec ? 1 : 0;
     a.scale_log2 = d->scale * 1.4426950408889634f;
     a.rope_mode = r ? r->mode : KD_FA_ROPE_NONE;
@@ -180,18 +203,18 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, void *ws, size_t ws_bytes, voi
     a.heads_inner = (a.m && d->mask.ne[2] == 1 && H > 1 && d->k.ne[1] <= 1024) ? 1 : 0;
 
     hipStream_t hs = static_cast<hipStream_t>(stream);
-    bool k_rope = rope_on;
-    if (ws && rope_on) {
+    bool k_rope = k_xform;
+    if (ws && k_xform) {
         const int hk = (int)d->k.ne[2], bk = (int)d->k.ne[3];
-        if (kdfa::launch_rope_k(a, d->k.type, hk, bk, ws, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
-        const int64_t row = kHeadDim * (int64_t)elem_size(d->k.type);
+        if (kdfa::launch_rope_k(a, d->v.type, hk, bk, ws, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
+        const int64_t row = kHeadDim * (int64_t)elem_size(d->v.type);
         a.k = static_cast<const char *>(ws);
         a.k_nb1 = row;
         a.k_nb2 = row * a.Lk;
         a.k_nb3 = row * a.Lk * hk;
         k_rope = false;
     }
-    if (kdfa::launch(a, d->k.type, k_rope, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
+    if (kdfa::launch(a, d->v.type, k_rope, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
     return KD_FA_OK;
 }
 
@@ -212,25 +235,37 @@ bool axes_ok(int T, int Hp, int Wp, const int axes[3]) {
 extern "C" {
 
 int kd_fa_supports(const kd_fa_desc *desc, int *reason) {
-    const int st = validate(desc, nullptr, nullptr);
+    const int st = validate(desc, nullptr, nullptr, nullptr);
     if (reason) *reason = st;
     return st == KD_FA_OK ? 1 : 0;
 }
 
 int kd_fa_rope_supports(const kd_fa_desc *desc, const kd_fa_rope *rope, int *reason) {
-    const int st = validate(desc, rope, nullptr);
+    const int st = validate(desc, rope, nullptr, nullptr);
     if (reason) *reason = st;
     return st == KD_FA_OK ? 1 : 0;
 }
 
-int kd_fa_run(const kd_fa_desc *desc, void *stream) { return run(desc, nullptr, nullptr, 0, stream); }
+int kd_fa_run(const kd_fa_desc *desc, void *stream) { return run(desc, nullptr, nullptr, nullptr, 0, stream); }
 
 int kd_fa_rope_run(const kd_fa_desc *desc, const kd_fa_rope *rope, void *stream) {
-    return run(desc, rope, nullptr, 0, stream);
+    return run(desc, rope, nullptr, nullptr, 0, stream);
+}
+
+int kd_fa_dit_supports(const kd_fa_desc *desc, const kd_fa_rope *rope, const kd_fa_qk_norm *norm,
+                       int *reason) {
+    const int st = validate(desc, rope, norm, nullptr, true);
+    if (reason) *reason = st;
+    return st == KD_FA_OK ? 1 : 0;
+}
+
+int kd_fa_dit_run(const kd_fa_desc *desc, const kd_fa_rope *rope, const kd_fa_qk_norm *norm,
+                  void *workspace, size_t workspace_bytes, void *stream) {
+    return run(desc, rope, norm, workspace, workspace_bytes, stream);
 }
 
 size_t kd_fa_rope_workspace_size(const kd_fa_desc *desc) {
-    if (!desc || validate(desc, nullptr, nullptr) != KD_FA_OK) return 0;
+    if (!desc || validate(desc, nullptr, nullptr, nullptr, true) != KD_FA_OK) return 0;
     return rope_ws_bytes(desc);
 }
 
@@ -238,7 +273,7 @@ int kd_fa_rope_run_ws(const kd_fa_desc *desc, const kd_fa_rope *rope, void *work
                       size_t workspace_bytes, void *stream) {
     if (!workspace && rope && rope->mode != KD_FA_ROPE_NONE && desc && desc->k.ne[1] > 0)
         return KD_FA_ERR_NULL;
-    return run(desc, rope, workspace, workspace_bytes, stream);
+    return run(desc, rope, nullptr, workspace, workspace_bytes, stream);
 }
 
 // rope::compute_visual_rope (src/rope.hpp:56-102).

@@ -27,6 +27,7 @@ struct Args {
     int32_t rv2, rv3;   // H / Hv, B / Bv
     int32_t m_ne2, m_ne3;
     int32_t q_type;     // KD_FA_TYPE_*
+    int32_t k_type;     // K as stored (F32 only for the K pre-pass)
     int32_t mask_vec;   // mask rows are 16-byte aligned
     float scale_log2;   // scale * log2(e)
     int32_t rope_mode;  // KD_FA_ROPE_*
@@ -39,14 +40,19 @@ struct Args {
     int32_t n_qt;       // query tiles per (b, h)
     int32_t n_blocks;   // n_qt * H * B
     int32_t heads_inner;  // block order: heads fastest (mask shared by all heads)
+    int32_t o_type;       // dst element type: F32, F16 or BF16
+    const float *qn_w;    // RMSNorm weight of Q (F32 [128]) or nullptr
+    const float *kn_w;    // RMSNorm weight of K (F32 [128]) or nullptr
+    float norm_eps;
 };
 
 // Enqueue the forward kernel for K/V element type kv_type on `stream`.
-// With a RoPE mode set, Q is rotated on load, and K too when k_rope.
+// Q is normalised (qn_w) and rotated (RoPE mode) on load; K too (kn_w,
+// RoPE mode) when k_rope.
 hipError_t launch(const Args &a, int kv_type, bool k_rope, hipStream_t stream);
 
-// Rotate K ([D, Lk, H/rk2, B/rk3] through a.k and its strides) into `out`,
-// contiguous, in K's type.
+// Normalise (kn_w) and rotate (RoPE mode) K ([D, Lk, H/rk2, B/rk3] through
+// a.k and its strides) into `out`, contiguous, in K's type.
 hipError_t launch_rope_k(const Args &a, int kv_type, int k_heads, int k_batch, void *out, hipStream_t stream);
 
 // Waves per workgroup (32 query rows each).

@@ -86,7 +86,7 @@ template <typename T, bool HAS_MASK, int RM, bool KROPE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void fa_fwd_d128(Args a) {
     constexpr bool ROPE = RM != KD_FA_ROPE_NONE;   // rotate Q on load
-    constexpr bool KR = ROPE && KROPE;              // rotate K tiles on load
+    constexpr bool KR = KROPE;                      // transform K tiles on load
     typedef Elem<T> E;
     typedef typename E::vec8 vec8;
     // four distinct LDS objects (not one array) so that the compiler can
@@ -137,11 +137,27 @@ void fa_fwd_d128(Args a) {
     {
         const char *qp = a.q + (int64_t)q_ld * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)b * a.q_nb3;
         const int esz = a.q_type == KD_FA_TYPE_F32 ? 4 : 2;
+        // RMSNorm of the row (query_norm): this lane holds 64 of its 128
+        // elements, the lane l ^ 32 the rest
+        float qscale = 1.0f;
+        if (a.qn_w) {
+            double ss = 0.0;
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+                float x[8];
+                load8_f32(qp + (ks * 16 + hi * 8) * esz, a.q_type, x);
+                ss += sum_sq8(x);
+            }
+            qscale = rms_scale(pair_sum_f64(ss), a.norm_eps);
+        }
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
             const int d0 = ks * 16 + hi * 8;
             float x[8];
             load8_f32(qp + d0 * esz, a.q_type, x);
+            if (a.qn_w)
+                rms_apply8(x, qscale, *reinterpret_cast<const f32x4 *>(a.qn_w + d0),
+                           *reinterpret_cast<const f32x4 *>(a.qn_w + d0 + 4));
             if (ROPE) {
                 const float *cp = rope_ptr<RM>(a, q_ld, d0);
                 rotate8(x, *reinterpret_cast<const f32x4 *>(cp), *reinterpret_cast<const f32x4 *>(cp + 4));
@@ -240,7 +256,9 @@ void fa_fwd_d128(Args a) {
             const int c = dma_pc ^ (r & 15);
             int kr = k_row_of(r);
             if (!full && t * kBN + kr >= Lk) kr = Lk - 1 - t * kBN;
-            if (RM == KD_FA_ROPE_TABLE) {
+            if (RM == KD_FA_ROPE_NONE) {
+                kreg[j] = ld16(kt + (full ? k_dma[j] : (uint32_t)kr * (uint32_t)a.k_nb1 + (c << 4)));
+            } else if (RM == KD_FA_ROPE_TABLE) {
                 const char *tt = reinterpret_cast<const char *>(a.rope_tab) + (int64_t)t * kBN * a.rope_nb1;
                 const uint32_t ko = full ? k_dma[j] : (uint32_t)kr * (uint32_t)a.k_nb1 + (c << 4);
                 const uint32_t to = full ? tab_off[j] : (uint32_t)kr * (uint32_t)a.rope_nb1 + (c << 5);
@@ -255,13 +273,23 @@ void fa_fwd_d128(Args a) {
             }
         }
     };
+    // key_norm weights of this lane's chunk (the chunk a lane handles is the
+    // same in every round: the row's low four bits do not change)
+    f32x4 kw0 = {}, kw1 = {};
+    if (KR && a.kn_w) {
+        const int c = dma_pc ^ ((4 * wave + dma_row) & 15);
+        kw0 = *reinterpret_cast<const f32x4 *>(a.kn_w + c * 8);
+        kw1 = *reinterpret_cast<const f32x4 *>(a.kn_w + c * 8 + 4);
+    }
     auto rope_store = [&](lds_t *dK) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < kRounds; ++j) {
             const int u = tid + kThreads * j;
             float x[8];
             for (int e = 0; e < 4; ++e) { x[2 * e] = E::lo(kreg[j][e]); x[2 * e + 1] = E::hi(kreg[j][e]); }
-            rotate8(x, kcs[j][0], kcs[j][1]);
+            // RMSNorm: the 16 lanes of a 16-lane group hold the 16 chunks of one row
+            if (a.kn_w) rms_apply8(x, rms_scale(sum16_f64(sum_sq8(x)), a.norm_eps), kw0, kw1);
+            if (ROPE) rotate8(x, kcs[j][0], kcs[j][1]);
             u32x4 w;
             for (int e = 0; e < 4; ++e) w[e] = E::pack2(x[2 * e], x[2 * e + 1]);
             *reinterpret_cast<__attribute__((address_space(3))) u32x4 *>(dK + u * 16) = w;
@@ -537,11 +565,12 @@ void fa_fwd_d128(Args a) {
         }
     }
 
-    // ---- epilogue: O / l -> dst[b][q][h][:] (F32) ---------------------------
+    // ---- epilogue: O / l -> dst[b][q][h][:] (F32, or rounded to F16 / BF16) --
     const float l_run = pair_sum(l_half);
     if (q_row < a.Lq) {
         const float inv = l_run == 0.0f ? 0.0f : 1.0f / l_run;
         char *op = a.o + (int64_t)b * a.o_nb3 + (int64_t)q_row * a.o_nb2 + (int64_t)h * a.o_nb1;
+        const int ot = a.o_type;
 #pragma unroll
         for (int dblk = 0; dblk < 4; ++dblk)
 #pragma unroll
@@ -549,7 +578,15 @@ void fa_fwd_d128(Args a) {
                 const int d = dblk * 32 + 8 * g + 4 * hi;
                 const f32x4 v = {o[dblk][4 * g] * inv, o[dblk][4 * g + 1] * inv,
                                  o[dblk][4 * g + 2] * inv, o[dblk][4 * g + 3] * inv};
-                *reinterpret_cast<f32x4 *>(op + d * 4) = v;
+                if (ot == KD_FA_TYPE_F32) {
+                    *reinterpret_cast<f32x4 *>(op + d * 4) = v;
+                } else if (ot == KD_FA_TYPE_BF16) {
+                    const u32x2 w = {Elem<__bf16>::pack2(v.x, v.y), Elem<__bf16>::pack2(v.z, v.w)};
+                    *reinterpret_cast<u32x2 *>(op + d * 2) = w;
+                } else {
+                    const u32x2 w = {Elem<_Float16>::pack2(v.x, v.y), Elem<_Float16>::pack2(v.z, v.w)};
+                    *reinterpret_cast<u32x2 *>(op + d * 2) = w;
+                }
             }
     }
 }
@@ -568,7 +605,7 @@ static hipError_t launch_r(const Args &a, bool k_rope, hipStream_t s) {
     case KD_FA_ROPE_AXES:
         return k_rope ? launch_t<T, M, KD_FA_ROPE_AXES, true>(a, s) : launch_t<T, M, KD_FA_ROPE_AXES, false>(a, s);
     default:
-        return launch_t<T, M, KD_FA_ROPE_NONE, false>(a, s);
+        return k_rope ? launch_t<T, M, KD_FA_ROPE_NONE, true>(a, s) : launch_t<T, M, KD_FA_ROPE_NONE, false>(a, s);
     }
 }
 
@@ -580,14 +617,19 @@ hipError_t launch(const Args &a, int kv_type, bool k_rope, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------
-// K pre-rotation: rope::apply on K (src/rope.hpp:109-155) with the same F32
-// arithmetic as the in-kernel rotation, rounded to K's type, written to a
-// contiguous [D, Lk, Hkv, Bk] buffer.  One thread per 16-byte chunk.
+// K pre-pass of the workspace entry points: ops::rms_norm (kn_w) and
+// rope::apply (src/rope.hpp:109-155) on K with the same F32 arithmetic as the
+// in-kernel transform, rounded to K's type, written to a contiguous
+// [D, Lk, Hkv, Bk] buffer in the operand type T (K may be stored in F32).
+// One thread per 8-element chunk; the 16 chunks of a row are 16 consecutive
+// lanes, which reduce the row's squares together.
 // ---------------------------------------------------------------------------
 template <typename T, int RM>
 __global__ __launch_bounds__(256) void rope_k_kernel(Args a, char *out, int64_t n_chunks) {
     typedef Elem<T> E;
     const int hk = a.H / a.rk2;   // K heads
+    // n_chunks is a multiple of 16 and so is every lane group's first index:
+    // the 16 lanes of a row enter and leave the loop together
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_chunks;
          i += (int64_t)gridDim.x * blockDim.x) {
         const int c = (int)(i & 15);
@@ -596,14 +638,36 @@ __global__ __launch_bounds__(256) void rope_k_kernel(Args a, char *out, int64_t 
         const int64_t hb = row / a.Lk;
         const int h = (int)(hb % hk);
         const int b = (int)(hb / hk);
-        const char *src = a.k + (int64_t)key * a.k_nb1 + (int64_t)h * a.k_nb2 + (int64_t)b * a.k_nb3 + c * 16;
-        u32x4 w = ld16(src);
+        const int esz = a.k_type == KD_FA_TYPE_F32 ? 4 : 2;
+        const char *src = a.k + (int64_t)key * a.k_nb1 + (int64_t)h * a.k_nb2 + (int64_t)b * a.k_nb3 + c * 8 * esz;
         float x[8];
-        for (int e = 0; e < 4; ++e) { x[2 * e] = E::lo(w[e]); x[2 * e + 1] = E::hi(w[e]); }
-        const float *cp = rope_ptr<RM>(a, key, c * 8);
-        rotate8(x, *reinterpret_cast<const f32x4 *>(cp), *reinterpret_cast<const f32x4 *>(cp + 4));
+        load8_f32(src, a.k_type, x);
+        u32x4 w;
+        if (a.kn_w)
+            rms_apply8(x, rms_scale(sum16_f64(sum_sq8(x)), a.norm_eps),
+                       *reinterpret_cast<const f32x4 *>(a.kn_w + c * 8),
+                       *reinterpret_cast<const f32x4 *>(a.kn_w + c * 8 + 4));
+        if (RM != KD_FA_ROPE_NONE) {
+            const float *cp = rope_ptr<RM>(a, key, c * 8);
+            rotate8(x, *reinterpret_cast<const f32x4 *>(cp), *reinterpret_cast<const f32x4 *>(cp + 4));
+        }
         for (int e = 0; e < 4; ++e) w[e] = E::pack2(x[2 * e], x[2 * e + 1]);
         *reinterpret_cast<u32x4 *>(out + i * 16) = w;
+    }
+}
+
+template <typename T>
+static void launch_rope_k_t(const Args &a, int grid, char *o, int64_t n_chunks, hipStream_t stream) {
+    switch (a.rope_mode) {
+    case KD_FA_ROPE_TABLE:
+        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_TABLE>), dim3(grid), dim3(256), 0, stream, a, o, n_chunks);
+        break;
+    case KD_FA_ROPE_AXES:
+        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_AXES>), dim3(grid), dim3(256), 0, stream, a, o, n_chunks);
+        break;
+    default:
+        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_NONE>), dim3(grid), dim3(256), 0, stream, a, o, n_chunks);
+        break;
     }
 }
 
@@ -613,17 +677,10 @@ hipError_t launch_rope_k(const Args &a, int kv_type, int k_heads, int k_batch, v
     const int64_t want = (n_chunks + 255) / 256;
     const int grid = (int)(want < 65536 ? want : 65536);
     char *o = static_cast<char *>(out);
-    if (kv_type == KD_FA_TYPE_BF16) {
-        if (a.rope_mode == KD_FA_ROPE_TABLE)
-            hipLaunchKernelGGL((rope_k_kernel<__bf16, KD_FA_ROPE_TABLE>), dim3(grid), dim3(256), 0, stream, a, o, n_chunks);
-        else
-            hipLaunchKernelGGL((rope_k_kernel<__bf16, KD_FA_ROPE_AXES>), dim3(grid), dim3(256), 0, stream, a, o, n_chunks);
-    } else {
-        if (a.rope_mode == KD_FA_ROPE_TABLE)
-            hipLaunchKernelGGL((rope_k_kernel<_Float16, KD_FA_ROPE_TABLE>), dim3(grid), dim3(256), 0, stream, a, o, n_chunks);
-        else
-            hipLaunchKernelGGL((rope_k_kernel<_Float16, KD_FA_ROPE_AXES>), dim3(grid), dim3(256), 0, stream, a, o, n_chunks);
-    }
+    if (kv_type == KD_FA_TYPE_BF16)
+        launch_rope_k_t<__bf16>(a, grid, o, n_chunks, stream);
+    else
+        launch_rope_k_t<_Float16>(a, grid, o, n_chunks, stream);
     return hipGetLastError();
 }
 

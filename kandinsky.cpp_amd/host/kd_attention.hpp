@@ -124,25 +124,40 @@ inline bool make_node(const Activation &q, const Activation &k, const Activation
 // ops::attention(ctx, backend, q, k, v, n_head, mask, flash=true,
 // causal=false) for one GPU stream.  q: [C, Lq, N]; k, v: [C_kv, Lk, N]
 // with C_kv = n_kv_head * d_head (grouped heads are broadcast by the op,
-// no repeat copies as ops.hpp:135-157 make); out: F32 [C, Lq, N].
+// no repeat copies as ops.hpp:135-157 make); out: [C, Lq, N], F32 (the
+// node's type) or, with out_type F16 / BF16, rounded to that type.
 // rope (optional): rotate Q and K on load (rope::apply, src/rope.hpp:109).
+// norm (optional): the query_norm / key_norm RMSNorm of the attention
+// modules before RoPE (crossdit.hpp:135-136, 192-193).
 inline Result attention(const Activation &q, const Activation &k, const Activation &v,
                         int64_t n_head, void *out, const Mask *mask = nullptr,
                         const kd_fa_rope *rope = nullptr, void *stream = nullptr,
-                        void *k_workspace = nullptr, size_t k_workspace_bytes = 0) {
+                        void *k_workspace = nullptr, size_t k_workspace_bytes = 0,
+                        const kd_fa_qk_norm *norm = nullptr, int32_t out_type = KD_FA_TYPE_F32) {
     Result r;
     kd_fa_desc d{};
     if (!make_node(q, k, v, n_head, out, mask, &d)) {
         r.status = KD_FA_ERR_SHAPE;
         return r;
     }
+    if (out_type != KD_FA_TYPE_F32) {
+        d.dst.type = out_type;
+        d.dst.nb[0] = 2;
+        d.dst.nb[1] = (size_t)d.dst.ne[0] * 2;
+        d.dst.nb[2] = d.dst.nb[1] * (size_t)d.dst.ne[1];
+        d.dst.nb[3] = d.dst.nb[2] * (size_t)d.dst.ne[2];
+    }
     int reason = KD_FA_OK;
-    const bool ok = rope ? kd_fa_rope_supports(&d, rope, &reason) : kd_fa_supports(&d, &reason);
+    const bool ok = norm ? kd_fa_dit_supports(&d, rope, norm, &reason)
+                  : rope ? kd_fa_rope_supports(&d, rope, &reason)
+                         : kd_fa_supports(&d, &reason);
     if (!ok) {
         r.status = reason;
         return r;
     }
-    if (rope && k_workspace)
+    if (norm)
+        r.status = kd_fa_dit_run(&d, rope, norm, k_workspace, k_workspace_bytes, stream);
+    else if (rope && k_workspace)
         r.status = kd_fa_rope_run_ws(&d, rope, k_workspace, k_workspace_bytes, stream);
     else if (rope)
         r.status = kd_fa_rope_run(&d, rope, stream);

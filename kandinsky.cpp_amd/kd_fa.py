@@ -90,6 +90,16 @@ class KdFaRope(ctypes.Structure):
     ]
 
 
+class KdFaQkNorm(ctypes.Structure):
+    """struct kd_fa_qk_norm: RMSNorm weights of the Q and K head rows."""
+
+    _fields_ = [
+        ("q_weight", ctypes.c_void_p),
+        ("k_weight", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+    ]
+
+
 class KdFaError(RuntimeError):
     def __init__(self, status: int, what: str = ""):
         self.status = status
@@ -119,6 +129,11 @@ def _lib():
         lib.kd_fa_rope_run.restype = ctypes.c_int
         lib.kd_fa_rope_run_ws.argtypes = [P(KdFaDesc), P(KdFaRope), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         lib.kd_fa_rope_run_ws.restype = ctypes.c_int
+        lib.kd_fa_dit_run.argtypes = [P(KdFaDesc), P(KdFaRope), P(KdFaQkNorm), ctypes.c_void_p, ctypes.c_size_t,
+                                      ctypes.c_void_p]
+        lib.kd_fa_dit_run.restype = ctypes.c_int
+        lib.kd_fa_dit_supports.argtypes = [P(KdFaDesc), P(KdFaRope), P(KdFaQkNorm), P(ctypes.c_int)]
+        lib.kd_fa_dit_supports.restype = ctypes.c_int
         lib.kd_fa_rope_workspace_size.argtypes = [P(KdFaDesc)]
         lib.kd_fa_rope_workspace_size.restype = ctypes.c_size_t
         fp = P(ctypes.c_float)
@@ -227,6 +242,17 @@ def rope_axes(axes_buf, grid, axes) -> KdFaRope:
     return r
 
 
+def qk_norm(q_weight=None, k_weight=None, eps=1e-6) -> KdFaQkNorm:
+    """RMSNorm descriptor over float32 (D,) device tensors (None: that side
+    is not normalised)."""
+    n = KdFaQkNorm()
+    n.q_weight = q_weight.data_ptr() if q_weight is not None else None
+    n.k_weight = k_weight.data_ptr() if k_weight is not None else None
+    n.eps = float(eps)
+    n._keep = (q_weight, k_weight)  # raw pointers: keep the tensors alive
+    return n
+
+
 def out_shape(q, v):
     """torch shape of dst for q (B, H, Lq, Dk) and v (Bk, Hkv, Lk, Dv)."""
     return (q.shape[0], q.shape[2], q.shape[1], v.shape[3])
@@ -250,11 +276,13 @@ def supports(q, k, v, mask=None, dst=None, scale=1.0, max_bias=0.0, logit_softca
     return bool(ok), reason.value
 
 
-def run_desc(desc: KdFaDesc, rope: KdFaRope | None = None, stream=None, workspace=None) -> int:
+def run_desc(desc: KdFaDesc, rope: KdFaRope | None = None, stream=None, workspace=None,
+             norm: KdFaQkNorm | None = None) -> int:
     """Enqueue on `stream` (a torch.cuda.Stream, a raw handle, or None for
     torch's current stream).  With `workspace` (a tensor of at least
     workspace_size(desc) bytes) the RoPE call pre-rotates K into it
-    (kd_fa_rope_run_ws).  Returns the status code."""
+    (kd_fa_rope_run_ws).  With `norm` the call is kd_fa_dit_run.  Returns
+    the status code."""
     torch = _torch()
     if stream is None:
         handle = torch.cuda.current_stream().cuda_stream
@@ -262,6 +290,12 @@ def run_desc(desc: KdFaDesc, rope: KdFaRope | None = None, stream=None, workspac
         handle = stream
     else:
         handle = stream.cuda_stream
+    if norm is not None:
+        wp, nbytes = None, 0
+        if workspace is not None:
+            wp, nbytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+        return _lib().kd_fa_dit_run(ctypes.byref(desc), ctypes.byref(rope) if rope is not None else None,
+                                    ctypes.byref(norm), ctypes.c_void_p(wp), nbytes, ctypes.c_void_p(handle))
     if rope is None:
         return _lib().kd_fa_run(ctypes.byref(desc), ctypes.c_void_p(handle))
     if workspace is not None:
@@ -278,20 +312,24 @@ def workspace_size(desc: KdFaDesc) -> int:
 
 
 def flash_attn_ext(q, k, v, mask=None, scale=None, max_bias=0.0, logit_softcap=0.0,
-                   dst=None, rope=None, stream=None, workspace=None):
-    """GGML_OP_FLASH_ATTN_EXT on the GPU; returns dst (B, Lq, H, Dv) float32.
+                   dst=None, rope=None, stream=None, workspace=None, norm=None, out_dtype=None):
+    """GGML_OP_FLASH_ATTN_EXT on the GPU; returns dst (B, Lq, H, Dv).
 
-    ``rope`` is a KdFaRope (rope_table / rope_axes) to rotate Q and K on load.
-    Raises KdFaError on any non-zero status (nothing is enqueued then)."""
+    ``rope`` is a KdFaRope (rope_table / rope_axes) to rotate Q and K on load;
+    ``norm`` a KdFaQkNorm (qk_norm) to RMS-normalise them first
+    (kd_fa_dit_run).  dst defaults to float32 (the node's type); ``out_dtype``
+    torch.bfloat16 / torch.float16 stores O rounded instead.  Raises
+    KdFaError on any non-zero status (nothing is enqueued then)."""
     torch = _torch()
     if scale is None:
         scale = 1.0 / float(q.shape[-1]) ** 0.5
     if dst is None:
-        dst = torch.empty(out_shape(q, v), dtype=torch.float32, device=q.device)
+        dst = torch.empty(out_shape(q, v), dtype=out_dtype or torch.float32, device=q.device)
     d = make_desc(q, k, v, mask, dst, scale, max_bias, logit_softcap)
-    st = run_desc(d, rope, stream, workspace)
+    st = run_desc(d, rope, stream, workspace, norm)
     if st != OK:
-        raise KdFaError(st, "kd_fa_rope_run" if rope is not None else "kd_fa_run")
+        name = "kd_fa_dit_run" if norm is not None else "kd_fa_rope_run" if rope is not None else "kd_fa_run"
+        raise KdFaError(st, name)
     return dst
 
 

@@ -186,6 +186,33 @@ void kdo_rope_apply_f32(const float *x, int64_t D, int64_t H, int64_t L,
             }
 }
 
+/* ggml_rms_norm followed by ggml_mul with the weight (ops::rms_norm,
+ * src/core/ops.hpp:76-80, of the RMSNorm module src/core/module.hpp:163-180
+ * that normalises each head row of Q and K, src/models/crossdit.hpp:135-136
+ * and 192-193, eps 1e-6).  Per row of D elements: the squares, each rounded
+ * to F32, summed in double; mean = (float)(sum / D); scale =
+ * 1.0f / sqrtf(mean + eps); y = x * scale, then z = y * w, each an F32
+ * operation as the two separate ggml ops round.  w == NULL skips the
+ * multiply.  Rows are contiguous ([rows][D]); out may alias x. */
+void kdo_rms_norm_mul(const float *x, int64_t rows, int64_t D, const float *w,
+                      float eps, float *out) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float *xr = x + r * D;
+        float *orow = out + r * D;
+        double sum = 0.0;
+        for (int64_t i = 0; i < D; ++i) {
+            const float sq = xr[i] * xr[i];
+            sum += (double)sq;
+        }
+        const float mean = (float)(sum / (double)D);
+        const float scale = 1.0f / sqrtf(mean + eps);
+        for (int64_t i = 0; i < D; ++i) {
+            const float y = xr[i] * scale;
+            orow[i] = w ? y * w[i] : y;
+        }
+    }
+}
+
 /* (cos, sin) of pair i for token idx under a RoPE descriptor whose data
  * pointers are host-readable. */
 static inline void rope_pair(const kd_fa_rope *r, int64_t idx, int64_t i,

@@ -9,6 +9,7 @@
  *   - IEEE half / bfloat16 conversions (round to nearest even);
  *   - rope::get_freqs, compute_text_rope, compute_visual_rope, apply
  *     (src/rope.hpp:23-155);
+ *   - ops::rms_norm: ggml_rms_norm + ggml_mul (src/core/ops.hpp:76-80);
  *   - kdo_fa_ggml: a restatement of ggml's per-row CPU flash-attention
  *     algorithm (ggml_compute_forward_flash_attn_ext_f16, the kernel the
  *     reference's CPU backend runs for the node built at
@@ -59,6 +60,10 @@ void kdo_rope_apply_f32(const float *x, int64_t D, int64_t H, int64_t L,
                         int64_t B, const float *table, float *out);
 
 /* Flat query-row id used by both oracle entry points (ggml's ir order). */
+/* ggml_rms_norm + ggml_mul by the weight over rows of D (ops.hpp:76-80). */
+void kdo_rms_norm_mul(const float *x, int64_t rows, int64_t D, const float *w,
+                      float eps, float *out);
+
 static inline int64_t kdo_row_id(int64_t b, int64_t h, int64_t i,
                                  int64_t H, int64_t Lq) {
     return i + Lq * (h + H * b);

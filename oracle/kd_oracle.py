@@ -71,6 +71,7 @@ def lib():
         L.kdo_rope_text_table.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_float, fp]
         L.kdo_rope_visual_table.argtypes = [ctypes.c_int] * 3 + [ip, fp, ctypes.c_float, fp]
         L.kdo_rope_apply_f32.argtypes = [fp] + [ctypes.c_int64] * 4 + [fp, fp]
+        L.kdo_rms_norm_mul.argtypes = [fp, ctypes.c_int64, ctypes.c_int64, fp, ctypes.c_float, fp]
         L.kdo_fa_ggml.argtypes = [P(Desc), P(Rope), ctypes.c_int, P(ctypes.c_int64), ctypes.c_int64, ctypes.c_int]
         L.kdo_fa_ggml.restype = ctypes.c_int
         L.kdo_fa_f64.argtypes = [P(Desc), P(Rope), P(ctypes.c_int64), ctypes.c_int64, dp, ctypes.c_int]
@@ -203,6 +204,20 @@ def rope_apply(x, table):
     out = np.empty_like(x)
     fp = ctypes.POINTER(ctypes.c_float)
     lib().kdo_rope_apply_f32(x.ctypes.data_as(fp), D, H, L, B, t.ctypes.data_as(fp), out.ctypes.data_as(fp))
+    return out
+
+
+def rms_norm(x, weight=None, eps=1e-6):
+    """ops::rms_norm (ggml_rms_norm + ggml_mul by weight) over the last axis
+    of float32 x; weight float32 (D,) or None."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    D = x.shape[-1]
+    rows = x.size // D if D else 0
+    out = np.empty_like(x)
+    fp = ctypes.POINTER(ctypes.c_float)
+    w = None if weight is None else np.ascontiguousarray(weight, dtype=np.float32)
+    lib().kdo_rms_norm_mul(x.ctypes.data_as(fp), rows, D, None if w is None else w.ctypes.data_as(fp),
+                           float(eps), out.ctypes.data_as(fp))
     return out
 
 

@@ -40,6 +40,8 @@ def test_struct_layout_matches_c():
              offsetof(kd_fa_desc, prec), sizeof(kd_fa_rope));
       printf("%zu %zu %zu %zu\n", offsetof(kd_fa_rope, table), offsetof(kd_fa_rope, axes_data),
              offsetof(kd_fa_rope, grid), offsetof(kd_fa_rope, axes));
+      printf("%zu %zu %zu\n", sizeof(kd_fa_qk_norm), offsetof(kd_fa_qk_norm, k_weight),
+             offsetof(kd_fa_qk_norm, eps));
       return 0;
     }
     """
@@ -53,7 +55,8 @@ def test_struct_layout_matches_c():
     T, Dd, R = kd_fa.KdFaTensor, kd_fa.KdFaDesc, kd_fa.KdFaRope
     want = [ctypes.sizeof(T), T.ne.offset, T.nb.offset, T.data.offset, ctypes.sizeof(Dd),
             Dd.dst.offset, Dd.scale.offset, Dd.prec.offset, ctypes.sizeof(R),
-            R.table.offset, R.axes_data.offset, R.grid.offset, R.axes.offset]
+            R.table.offset, R.axes_data.offset, R.grid.offset, R.axes.offset,
+            ctypes.sizeof(kd_fa.KdFaQkNorm), kd_fa.KdFaQkNorm.k_weight.offset, kd_fa.KdFaQkNorm.eps.offset]
     assert got == want
 
 
@@ -110,7 +113,12 @@ def test_rejections_carry_reason():
     assert _sup(q, k, v, m, dst, scale=float("nan")) == (False, kd_fa.ERR_PARAM)
     assert _sup(q, k.float(), v.float(), m, dst) == (False, kd_fa.ERR_TYPE)          # F32 K
     assert _sup(q, k, v.to(torch.bfloat16), m, dst) == (False, kd_fa.ERR_TYPE)       # V type != K type
-    assert _sup(q, k, v, m, dst.half()) == (False, kd_fa.ERR_TYPE)                   # F16 dst
+    assert _sup(q, k, v, m, dst.half()) == (True, 0)                                 # F16 dst: a fused cast
+    assert _sup(q, k, v, m, dst.bfloat16()) == (True, 0)                             # BF16 dst
+    d = kd_fa.make_desc(q, k, v, m, dst, 0.1)
+    d.dst.type = 8                                                                   # a quantised type
+    reason = ctypes.c_int(0)
+    assert kd_fa.lib().kd_fa_supports(ctypes.byref(d), ctypes.byref(reason)) == 0 and reason.value == kd_fa.ERR_TYPE
     assert _sup(q, k, v, torch.zeros((1, 1, 64, 48)), dst) == (False, kd_fa.ERR_TYPE)  # F32 mask
     assert _sup(q, k, v, torch.zeros((1, 1, 63, 48), dtype=torch.float16), dst) == (False, kd_fa.ERR_SHAPE)
     assert _sup(q, k, v, torch.zeros((1, 1, 64, 47), dtype=torch.float16), dst) == (False, kd_fa.ERR_SHAPE)
@@ -182,3 +190,24 @@ def test_workspace_size_and_null_workspace():
     assert kd_fa.workspace_size(bad) == 0
     rope = kd_fa.rope_table(torch.zeros((60, 128)))
     assert kd_fa.lib().kd_fa_rope_run_ws(ctypes.byref(d), ctypes.byref(rope), None, 0, None) == kd_fa.ERR_NULL
+
+
+def test_norm_descriptor_checks():
+    q, k, v, m, dst = _node(Lq=60, Lk=60, qt=torch.float32, kt=torch.bfloat16)
+    w = torch.ones(132)
+    sup = kd_fa.lib().kd_fa_dit_supports
+
+    def ask(norm, rope=None):
+        d = kd_fa.make_desc(q, k, v, None, dst, 0.1)
+        reason = ctypes.c_int(0)
+        ok = sup(ctypes.byref(d), ctypes.byref(rope) if rope is not None else None,
+                 ctypes.byref(norm) if norm is not None else None, ctypes.byref(reason))
+        return bool(ok), reason.value
+
+    assert ask(None) == (True, 0)
+    assert ask(kd_fa.qk_norm(w[:128], w[:128])) == (True, 0)
+    assert ask(kd_fa.qk_norm(None, w[:128], 1e-5)) == (True, 0)
+    assert ask(kd_fa.qk_norm(w[:128], None), kd_fa.rope_table(torch.zeros((60, 128)))) == (True, 0)
+    assert ask(kd_fa.qk_norm(w[1:129], w[:128])) == (False, kd_fa.ERR_LAYOUT)     # 4-byte aligned weight
+    assert ask(kd_fa.qk_norm(w[:128], w[:128], float("nan"))) == (False, kd_fa.ERR_ROPE)
+    assert ask(kd_fa.qk_norm(w[:128], w[:128], -1.0)) == (False, kd_fa.ERR_ROPE)

@@ -290,10 +290,12 @@ def test_self_attention_production_sampled(cfg):
     print(f"[{name}] {m}", flush=True)
 
 
-def test_cpp_ops_attention_mirror_on_gpu(tmp_path):
+@pytest.mark.parametrize("with_norm", [False, True])
+def test_cpp_ops_attention_mirror_on_gpu(tmp_path, with_norm):
     """kd::attention (C++ mirror of ops::attention) on the reference's
     activation layout q [C, Lq, N] F32, k/v [C, Lk, N] bf16, with the RoPE
-    table, run by the compiled driver kandinsky.cpp_amd/kd_attention_run."""
+    table (and the query/key RMSNorm, K through a workspace), run by the
+    compiled driver kandinsky.cpp_amd/kd_attention_run."""
     import os
     import subprocess
     _need_gpu()
@@ -313,12 +315,22 @@ def test_cpp_ops_attention_mirror_on_gpu(tmp_path):
     ka.view(torch.int16).numpy().tofile(files["k"])
     va.view(torch.int16).numpy().tofile(files["v"])
     table.tofile(files["r"])
-    res = subprocess.run([exe, str(H), str(L), str(L), str(N), "bf16", files["q"], files["k"],
-                          files["v"], files["o"], files["r"]], capture_output=True, text=True, timeout=60)
+    args = [exe, str(H), str(L), str(L), str(N), "bf16", files["q"], files["k"], files["v"], files["o"], files["r"]]
+    wq = (torch.randn(D, generator=g) * 0.3 + 1.0).float()
+    wk = (torch.randn(D, generator=g) * 0.3 + 1.0).float()
+    if with_norm:
+        wq.numpy().tofile(str(tmp_path / "wq.bin"))
+        wk.numpy().tofile(str(tmp_path / "wk.bin"))
+        args += [str(tmp_path / "wq.bin"), str(tmp_path / "wk.bin")]
+    res = subprocess.run(args, capture_output=True, text=True, timeout=60)
     assert res.returncode == 0, res.stderr
     out = torch.from_numpy(np.fromfile(files["o"], dtype=np.float32).reshape(N, L, H, D))
     q4 = qa.view(N, L, H, D).permute(0, 2, 1, 3).contiguous()
     k4 = ka.view(N, L, H, D).permute(0, 2, 1, 3).contiguous()
     v4 = va.view(N, L, H, D).permute(0, 2, 1, 3).contiguous()
-    ref = orc.fa_f64(q4, k4, v4, rope=orc.rope_table(torch.from_numpy(table)))
+    if with_norm:
+        q4 = torch.from_numpy(orc.rms_norm(q4.numpy(), wq.numpy(), 1e-6))
+        k4 = torch.from_numpy(orc.rms_norm(k4.float().numpy(), wk.numpy(), 1e-6))
+    ref = orc.fa_f64(q4, k4.to(torch.bfloat16) if with_norm else k4, v4,
+                     rope=orc.rope_table(torch.from_numpy(table)))
     assert_parity(gather_rows(out, np.arange(N * H * L), H, L), ref, "C++ mirror")
