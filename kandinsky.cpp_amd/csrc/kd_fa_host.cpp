@@ -56,7 +56,7 @@ int validate(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, b
     if (H % k.ne[2] || H % v.ne[2] || B % k.ne[3] || B % v.ne[3]) return KD_FA_ERR_SHAPE;
     if (o.ne[0] != v.ne[0] || o.ne[1] != H || o.ne[2] != Lq || o.ne[3] != B) return KD_FA_ERR_SHAPE;
     if (Lq > kI32Max || Lk > kI32Max || H > kI32Max || B > kI32Max) return KD_FA_ERR_SHAPE;
-    const int64_t n_qt = (Lq + kdfa::kBlockM - 1) / kdfa::kBlockM;
+    const int64_t n_qt = (Lq + kdfa::kMinBlockRows - 1) / kdfa::kMinBlockRows;
     if (H > 0 && B > 0 && n_qt > kI32Max / H / B) return KD_FA_ERR_SHAPE;
     if (m.data) {
         if (m.ne[0] < Lk || m.ne[1] < Lq || m.ne[2] <= 0 || m.ne[3] <= 0) return KD_FA_ERR_SHAPE;
@@ -195,15 +195,16 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
         a.rcp_h = 1.0f / (float)r->grid[1];
         a.rcp_w = 1.0f / (float)r->grid[2];
     }
-    a.n_qt = (int32_t)((Lq + kdfa::kBlockM - 1) / kdfa::kBlockM);
+    hipStream_t hs = static_cast<hipStream_t>(stream);
+    bool k_rope = k_xform && !ws;
+    const int rows = kdfa::block_rows(a.m != nullptr, k_rope);
+    a.n_qt = (int32_t)((Lq + rows - 1) / rows);
     a.n_blocks = (int32_t)(a.n_qt * H * B);
     // a mask row block shared by every head is read once per q-tile when the
     // heads of a q-tile run back to back (K and V of all heads then share the
     // L2 instead, which the short text keys of the cross-attention allow)
     a.heads_inner = (a.m && d->mask.ne[2] == 1 && H > 1 && d->k.ne[1] <= 1024) ? 1 : 0;
 
-    hipStream_t hs = static_cast<hipStream_t>(stream);
-    bool k_rope = k_xform;
     if (ws && k_xform) {
         const int hk = (int)d->k.ne[2], bk = (int)d->k.ne[3];
         if (kdfa::launch_rope_k(a, d->v.type, hk, bk, ws, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
@@ -212,7 +213,6 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
         a.k_nb1 = row;
         a.k_nb2 = row * a.Lk;
         a.k_nb3 = row * a.Lk * hk;
-        k_rope = false;
     }
     if (kdfa::launch(a, d->v.type, k_rope, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
     return KD_FA_OK;

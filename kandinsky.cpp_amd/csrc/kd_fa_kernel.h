@@ -55,10 +55,12 @@ hipError_t launch(const Args &a, int kv_type, bool k_rope, hipStream_t stream);
 // a.k and its strides) into `out`, contiguous, in K's type.
 hipError_t launch_rope_k(const Args &a, int kv_type, int k_heads, int k_batch, void *out, hipStream_t stream);
 
-// Waves per workgroup (32 query rows each).
-#ifndef KD_FA_WAVES
-#define KD_FA_WAVES 8
-#endif
-constexpr int kBlockM = 32 * KD_FA_WAVES;
+// Waves per workgroup (32 query rows each): 8 (two waves per SIMD) for the
+// unmasked kernels; 4 for the plain masked one -- the short text
+// cross-attention, where two independent workgroups per CU hide each
+// other's Q load and O store.
+constexpr int waves_per_block(bool masked, bool k_on_load) { return masked && !k_on_load ? 4 : 8; }
+constexpr int block_rows(bool masked, bool k_on_load) { return 32 * waves_per_block(masked, k_on_load); }
+constexpr int kMinBlockRows = 128;
 
 }  // namespace kdfa

@@ -31,16 +31,9 @@
 
 namespace kdfa {
 
-constexpr int kWaves = KD_FA_WAVES;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kBM = 32 * kWaves; // query rows per workgroup
 
 constexpr int kBN = 64;                             // keys per tile
 constexpr int kTileBytes = kBN * kD * 2;            // one K or V tile
-constexpr int kRounds = kTileBytes / (kThreads * 16);  // 16-byte DMA rounds per thread per tile
-
-static_assert(kBM == kBlockM, "block rows");
-static_assert(kRounds * kThreads * 16 == kTileBytes, "tile shape");
 
 template <bool B> struct BC { static constexpr bool value = B; };
 
@@ -83,10 +76,15 @@ template <int PRE> __device__ __forceinline__ void sched_qk() {
 #endif
 
 template <typename T, bool HAS_MASK, int RM, bool KROPE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(64 * waves_per_block(HAS_MASK, KROPE)) __attribute__((amdgpu_waves_per_eu(2)))
 void fa_fwd_d128(Args a) {
     constexpr bool ROPE = RM != KD_FA_ROPE_NONE;   // rotate Q on load
     constexpr bool KR = KROPE;                      // transform K tiles on load
+    constexpr int kWaves = waves_per_block(HAS_MASK, KROPE);
+    constexpr int kThreads = 64 * kWaves;
+    constexpr int kBM = 32 * kWaves;                // query rows per workgroup
+    constexpr int kRounds = kTileBytes / (kThreads * 16);  // 16-byte DMA rounds per thread per tile
+    static_assert(kRounds * kThreads * 16 == kTileBytes, "tile shape");
     typedef Elem<T> E;
     typedef typename E::vec8 vec8;
     // four distinct LDS objects (not one array) so that the compiler can
@@ -593,7 +591,7 @@ void fa_fwd_d128(Args a) {
 
 template <typename T, bool M, int R, bool KR>
 static hipError_t launch_t(const Args &a, hipStream_t stream) {
-    hipLaunchKernelGGL((fa_fwd_d128<T, M, R, KR>), dim3(a.n_blocks), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((fa_fwd_d128<T, M, R, KR>), dim3(a.n_blocks), dim3(64 * waves_per_block(M, KR)), 0, stream, a);
     return hipGetLastError();
 }
 
