@@ -1,0 +1,582 @@
+#!/usr/bin/env python3
+"""Writes kd_fa_w64_loop.inc: the key loop of fa_fwd_w64 (64 query rows per
+wave, one wave per SIMD) as inline-asm strings, one per operand type.
+
+The loop is scheduled by hand because its two ingredients need registers
+that the compiler does not give it: O (64 rows x 128 floats per wave = 128
+accumulation registers) and Q (64 registers) stay in AGPRs as MFMA
+operands, and the softmax of one tile runs between the matrix products of
+another tile of the same wave.  Per 64-key tile t (step t):
+
+  phase 1   MFMA  S(t+1) = K(t+1) Q^T       32 x 32x32x16, K fragments from LDS
+            VALU  softmax of S(t), keys 32-63   (exp2, round to T, row sums)
+  check     a row whose weight sum left [0, 2^64]: exact max, rescale, redo
+  phase 2   MFMA  O^T += V(t)^T P(t)^T       32 x 32x32x16, V^T by ds_read_b64_tr_b16
+            VALU  softmax of S(t+1), keys 0-31
+
+Every arithmetic step is the one the 32-row kernel (kd_fa_kernel.hip)
+performs, in the same order per row -- the same MFMA accumulation order over
+k-steps and key steps, the same fma / exp2 / rounding, the same row sums
+(one dot2 chain per 16-key step, combined as (s0 + s1) + (s2 + s3)), the
+same lazy-max rule decided per 32-row block -- so the two kernels give
+bitwise identical results.
+
+The generator also enforces the issue rules of the code it writes: wait
+states between an MFMA result and its non-MFMA readers, VALU results and
+MFMA or permlane readers, transcendental results and their readers, dot2
+results and their readers (the hardware does not hold back a dependent
+instruction there: without them the reader sees the value from before the
+dot2), M0 and the LDS DMA that reads it; and an lgkmcnt wait before the
+first use of every LDS load (at most 15 in flight).
+
+Usage: python3 gen_w64_loop.py [out]  (default: kd_fa_w64_loop.inc beside it)
+"""
+import os
+import re
+
+# ---------------------------------------------------------------- registers
+# VGPRs v24..v247 belong to the loop; the compiler keeps v0..v23 and
+# v248..v255 for the operands and its own values.
+S_BASE = (24, 88)      # S[parity]: [qb][kb] -> +32*qb + 16*kb, 16 floats
+P_BASE = (152, 184)    # P[parity]: [qb][kst] -> +16*qb + 4*kst, 4 words
+T_BASE = 216           # 4 fma results
+E_BASE = 220           # 8 exp results
+M = (228, 229)         # running max per query block (log2 units)
+LH = (230, 231)        # running half-row weight sum
+# per query block: the tile's half-row weight sum (keys 0-31 first, then all
+# 64) and two partial sums of 16-key steps
+PS = ((232, 233, 234), (235, 236, 237))
+X, Y = 238, 239
+ONE = 240              # the operand-type pair (1, 1)
+W_BASE = 241           # 7 slow-path temporaries (241..247)
+V_LAST = 247
+# AGPRs
+A_O = 0                # O[qb][dblk] -> +64*qb + 16*dblk, 16 floats
+A_Q = 128              # Q[qb][ks] -> +32*qb + 4*ks
+A_KF = 192             # K fragments: 3 slots x 2 key blocks x 4
+A_VF = 216             # V^T fragments: 4 slots x 4
+A_LAST = 231
+# SGPRs s84..s95
+S_K = 84               # s[84:87] K buffer resource (moves one tile per DMA)
+S_V = 88               # s[88:91] V buffer resource
+S_T = 92               # step counter
+S_TMP = 93
+S_VCC = 94             # s[94:95]: the row check's lane mask
+S_FIRST, S_LAST = 84, 95
+
+# LDS layout (bytes from the workgroup's array)
+KBUF = (0, 16384)
+VBUF = (32768, 49152)
+Q_OFF = 65536
+
+MFMA_WS = 20           # MFMA result -> VALU / LDS / accvgpr access
+VALU_MFMA_WS = 4       # VALU or accvgpr write -> MFMA operand read
+TRANS_WS = 2           # v_exp result -> reader
+DOT_WS = 3             # v_dot2 result -> reader other than a dot2 accumulating on it
+DOT_ACC_WS = 2         # v_dot2 result -> the next dot2 of its chain
+PERM_WS = 2            # VALU write -> v_permlane32_swap read
+M0_WS = 1              # m0 write -> LDS DMA
+
+
+def vr(i):
+    return f"v{i}"
+
+
+def vrng(b, n):
+    return f"v[{b}:{b + n - 1}]"
+
+
+def arng(b, n):
+    return f"a[{b}:{b + n - 1}]"
+
+
+def vset(b, n):
+    return {f"v{i}" for i in range(b, b + n)}
+
+
+def aset(b, n):
+    return {f"a{i}" for i in range(b, b + n)}
+
+
+class Ins:
+    """One instruction: text, kind, registers read and written."""
+
+    def __init__(self, text, kind, rd=(), wr=(), m0w=False, m0r=False):
+        self.text, self.kind = text, kind
+        self.rd, self.wr = set(rd), set(wr)
+        self.m0w, self.m0r = m0w, m0r
+
+
+def valu(text, rd, wr):
+    return Ins(text, "valu", rd, wr)
+
+
+class Tracker:
+    """Inserts s_nop / s_waitcnt lgkmcnt in straight-line code."""
+
+    def __init__(self):
+        self.out = []
+        self.pos = 0
+        self.mfma_w = {}
+        self.valu_w = {}
+        self.trans_w = {}
+        self.dot_w = {}
+        self.m0_w = -100
+        self.lds = []       # pending LDS ops: (regs written, regs read)
+
+    def _nop(self, n):
+        while n > 0:
+            k = min(n, 8)
+            self.out.append(f"s_nop {k - 1}")
+            self.pos += k
+            n -= k
+
+    def _wait_lgkm(self, keep):
+        self.out.append(f"s_waitcnt lgkmcnt({keep})")
+        self.pos += 1
+        self.lds = self.lds[len(self.lds) - keep:] if keep else []
+
+    def label(self, name):
+        self.out.append(f"{name}:")
+
+    def raw(self, text, ws=1):
+        self.out.append(text)
+        self.pos += ws
+
+    def emit(self, i):
+        touched = i.rd | i.wr
+        # LDS results: wait for the last pending load this instruction touches
+        last = -1
+        for k, (w, r) in enumerate(self.lds):
+            if (w & touched) or (r & i.wr):
+                last = k
+        if last >= 0:
+            self._wait_lgkm(len(self.lds) - last - 1)
+        if i.kind in ("lds_rd", "lds_wr") and len(self.lds) >= 15:
+            self._wait_lgkm(14)
+        need = 0
+        if i.kind != "mfma":
+            for r in touched:
+                if r in self.mfma_w:
+                    need = max(need, MFMA_WS - (self.pos - self.mfma_w[r] - 1))
+        else:
+            for r in i.rd:
+                if r in self.valu_w:
+                    need = max(need, VALU_MFMA_WS - (self.pos - self.valu_w[r] - 1))
+        for r in i.rd:
+            if r in self.trans_w:
+                need = max(need, TRANS_WS - (self.pos - self.trans_w[r] - 1))
+        for r in i.rd:
+            if r in self.dot_w:
+                ws = DOT_ACC_WS if (i.kind == "dot" and r in i.wr) else DOT_WS
+                need = max(need, ws - (self.pos - self.dot_w[r] - 1))
+        if i.kind == "perm":
+            for r in i.rd:
+                if r in self.valu_w:
+                    need = max(need, PERM_WS - (self.pos - self.valu_w[r] - 1))
+        if i.m0r:
+            need = max(need, M0_WS - (self.pos - self.m0_w - 1))
+        if need > 0:
+            self._nop(need)
+        self.out.append(i.text)
+        p = self.pos
+        self.pos += 1
+        if i.m0w:
+            self.m0_w = p
+        for r in i.wr:
+            self.mfma_w.pop(r, None)
+            self.valu_w.pop(r, None)
+            self.trans_w.pop(r, None)
+            self.dot_w.pop(r, None)
+        if i.kind == "mfma":
+            for r in i.wr:
+                self.mfma_w[r] = p
+        elif i.kind in ("valu", "trans", "perm", "accw", "dot"):
+            for r in i.wr:
+                self.valu_w[r] = p
+            if i.kind == "trans":
+                for r in i.wr:
+                    self.trans_w[r] = p
+            if i.kind == "dot":
+                for r in i.wr:
+                    self.dot_w[r] = p
+        if i.kind == "lds_rd":
+            self.lds.append((set(i.wr), set()))
+        elif i.kind == "lds_wr":
+            self.lds.append((set(), set(i.rd)))
+
+    def settle(self):
+        """Forget hazards older than any rule's window (after barriers)."""
+        horizon = self.pos - 64
+        for d in (self.mfma_w, self.valu_w, self.trans_w, self.dot_w):
+            for r in [r for r, p in d.items() if p < horizon]:
+                del d[r]
+
+
+class Gen:
+    def __init__(self, T):
+        self.T = T
+        self.mfma = f"v_mfma_f32_32x32x16_{T}"
+        self.cvt = {"bf16": "v_cvt_pk_bf16_f32", "f16": "v_cvt_pk_f16_f32"}[T]
+        self.dot, self.one = {"bf16": ("v_dot2c_f32_bf16", "0x3f803f80"),
+                              "f16": ("v_dot2c_f32_f16", "0x3c003c00")}[T]
+        self.dot3 = {"bf16": "v_dot2_f32_bf16", "f16": "v_dot2_f32_f16"}[T]
+        self.slow = []      # out-of-line blocks (lists of lines)
+
+    # ---------------------------------------------------------- streams
+    def qk_stream(self, kbuf, sp):
+        """S[sp] = K(kbuf) Q^T: (pre-reads, [(reads before, mfma)])."""
+        reads = {}
+        for ks in range(8):
+            slot = ks % 3
+            reads[ks] = [Ins(f"ds_read_b128 {arng(A_KF + 8 * slot + 4 * kb, 4)}, %[krd{ks}] offset:{kbuf + kb * 8192}",
+                             "lds_rd", (), aset(A_KF + 8 * slot + 4 * kb, 4)) for kb in range(2)]
+        pre = reads[0] + reads[1]
+        seq = []
+        for ks in range(8):
+            slot = ks % 3
+            n = 0
+            for kb in range(2):
+                for qb in range(2):
+                    d = S_BASE[sp] + 32 * qb + 16 * kb
+                    a = A_KF + 8 * slot + 4 * kb
+                    b = A_Q + 32 * qb + 4 * ks
+                    c = "0" if ks == 0 else vrng(d, 16)
+                    rd = aset(a, 4) | aset(b, 4) | (set() if ks == 0 else vset(d, 16))
+                    before = reads[ks + 2] if (n == 1 and ks + 2 < 8) else []
+                    seq.append((before, Ins(f"{self.mfma} {vrng(d, 16)}, {arng(a, 4)}, {arng(b, 4)}, {c}",
+                                            "mfma", rd, vset(d, 16))))
+                    n += 1
+        return pre, seq
+
+    def pv_stream(self, vbuf, pp):
+        """O += V(vbuf)^T P[pp]^T: (pre-reads, [(reads before, mfma)])."""
+        def frag_reads(f):
+            kst, dblk = divmod(f, 4)
+            s = A_VF + 4 * (f % 4)
+            off = vbuf + 4096 * kst
+            return [Ins(f"ds_read_b64_tr_b16 {arng(s, 2)}, %[vrd{dblk}] offset:{off}", "lds_rd", (), aset(s, 2)),
+                    Ins(f"ds_read_b64_tr_b16 {arng(s + 2, 2)}, %[vrd{dblk}] offset:{off + 1024}", "lds_rd", (),
+                        aset(s + 2, 2))]
+        pre = frag_reads(0) + frag_reads(1)
+        seq = []
+        for f in range(16):
+            kst, dblk = divmod(f, 4)
+            s = A_VF + 4 * (f % 4)
+            for qb in range(2):
+                o = A_O + 64 * qb + 16 * dblk
+                p = P_BASE[pp] + 16 * qb + 4 * kst
+                before = frag_reads(f + 2) if (qb == 1 and f + 2 < 16) else []
+                seq.append((before, Ins(f"{self.mfma} {arng(o, 16)}, {arng(s, 4)}, {vrng(p, 4)}, {arng(o, 16)}",
+                                        "mfma", aset(o, 16) | aset(s, 4) | vset(p, 4), aset(o, 16))))
+        return pre, seq
+
+    def softmax_half(self, sp, pp, half, qbs, finish):
+        """VALU stream: weights of keys 32*half .. +31 of S[sp] for the query
+        blocks qbs (pairs of blocks interleaved), rounded into P[pp]; each
+        16-key step's row sum is a 4-long dot2 chain.  finish: half 0 leaves
+        s0 + s1 in PS[qb][0]; half 1 leaves (s0 + s1) + (s2 + s3) there."""
+        pairs = [(qb, k) for k in range(8) for qb in qbs]
+        n = len(pairs)
+        out = []
+        for i in range(n + 2):
+            if i < n:
+                qb, k = pairs[i]
+                sb = S_BASE[sp] + 32 * qb + 16 * half
+                t = T_BASE + 2 * (i % 2)
+                for h in range(2):
+                    out.append(valu(f"v_fma_f32 {vr(t + h)}, {vr(sb + 2 * k + h)}, |%[c2]|, -{vr(M[qb])}",
+                                    {vr(sb + 2 * k + h), vr(M[qb])}, {vr(t + h)}))
+            if 1 <= i <= n:
+                t = T_BASE + 2 * ((i - 1) % 2)
+                e = E_BASE + 2 * ((i - 1) % 4)
+                for h in range(2):
+                    out.append(Ins(f"v_exp_f32 {vr(e + h)}, {vr(t + h)}", "trans", {vr(t + h)}, {vr(e + h)}))
+            if i >= 2:
+                qb, k = pairs[i - 2]
+                e = E_BASE + 2 * ((i - 2) % 4)
+                kst, j = 2 * half + k // 4, k % 4
+                w = P_BASE[pp] + 16 * qb + 4 * kst + j
+                acc = PS[qb][1 + (kst & 1)]
+                out.append(valu(f"{self.cvt} {vr(w)}, {vr(e)}, {vr(e + 1)}", {vr(e), vr(e + 1)}, {vr(w)}))
+                if j == 0:
+                    out.append(Ins(f"{self.dot3} {vr(acc)}, {vr(w)}, {vr(ONE)}, 0", "dot", {vr(w), vr(ONE)}, {vr(acc)}))
+                else:
+                    out.append(Ins(f"{self.dot} {vr(acc)}, {self.one}, {vr(w)}", "dot", {vr(w), vr(acc)}, {vr(acc)}))
+        for qb in qbs:
+            h01, a, b = PS[qb]
+            if half == 0:
+                out.append(valu(f"v_add_f32 {vr(h01)}, {vr(a)}, {vr(b)}", {vr(a), vr(b)}, {vr(h01)}))
+            else:
+                out.append(valu(f"v_add_f32 {vr(a)}, {vr(a)}, {vr(b)}", {vr(a), vr(b)}, {vr(a)}))
+                out.append(valu(f"v_add_f32 {vr(h01)}, {vr(h01)}, {vr(a)}", {vr(a), vr(h01)}, {vr(h01)}))
+        return out
+
+    def dma(self, which, buf, j):
+        base = S_K if which == "k" else S_V
+        return [Ins(f"s_add_u32 m0, %[dmab], {buf + 4096 * j}", "salu", m0w=True),
+                Ins(f"buffer_load_dwordx4 %[{which}dma{j}], s[{base}:{base + 3}], 0 offen lds", "vmem", m0r=True)]
+
+    def advance(self, which):
+        base = S_K if which == "k" else S_V
+        tile = "%[ktile]" if which == "k" else "%[vtile]"
+        return [Ins(f"s_add_u32 s{base}, s{base}, {tile}", "salu"),
+                Ins(f"s_addc_u32 s{base + 1}, s{base + 1}, 0", "salu"),
+                Ins(f"s_sub_u32 s{base + 2}, s{base + 2}, {tile}", "salu"),
+                Ins(f"s_cselect_b32 s{base + 2}, 0, s{base + 2}", "salu")]
+
+    # ------------------------------------------------------------ pieces
+    def merge(self, tr, seq, valus, extra=(), per=3):
+        """MFMAs in order, reads ahead of them, `per` VALU after each,
+        `extra` (SALU/VMEM groups) one group after each of the first MFMAs."""
+        vi = 0
+        extra = list(extra)
+        for n, (before, m) in enumerate(seq):
+            for r in before:
+                tr.emit(r)
+            tr.emit(m)
+            if n >= 1 and extra:
+                for x in extra.pop(0):
+                    tr.emit(x)
+            for _ in range(per):
+                if vi < len(valus):
+                    tr.emit(valus[vi])
+                    vi += 1
+        for grp in extra:
+            for x in grp:
+                tr.emit(x)
+        while vi < len(valus):
+            tr.emit(valus[vi])
+            vi += 1
+
+    def check(self, tr, p, tag):
+        """Row-sum check of both query blocks: one v_permlane32_swap of the
+        two blocks' half sums gives block 0's row sums in lanes 0-31 and
+        block 1's in lanes 32-63; the slow paths are out of line."""
+        slow, back = f".Lw64_slow_{tag}_%=", f".Lw64_back_{tag}_%="
+        s0, s1 = PS[0][0], PS[1][0]
+        tr.emit(valu(f"v_mov_b32 {vr(X)}, {vr(s0)}", {vr(s0)}, {vr(X)}))
+        tr.emit(valu(f"v_mov_b32 {vr(Y)}, {vr(s1)}", {vr(s1)}, {vr(Y)}))
+        tr.emit(Ins(f"v_permlane32_swap_b32 {vr(X)}, {vr(Y)}", "perm", {vr(X), vr(Y)}, {vr(X), vr(Y)}))
+        tr.emit(valu(f"v_add_f32 {vr(X)}, {vr(X)}, {vr(Y)}", {vr(X), vr(Y)}, {vr(X)}))
+        tr.emit(valu(f"v_cmp_nge_f32 vcc, 0x5f800000, {vr(X)}", {vr(X)}, ()))
+        tr.emit(Ins(f"s_cbranch_vccnz {slow}", "branch"))
+        tr.label(back)
+        for qb in range(2):
+            tr.emit(valu(f"v_add_f32 {vr(LH[qb])}, {vr(LH[qb])}, {vr(PS[qb][0])}", {vr(LH[qb]), vr(PS[qb][0])},
+                         {vr(LH[qb])}))
+        blk = [f"{slow}:", f"s_mov_b64 s[{S_VCC}:{S_VCC + 1}], vcc"]
+        for qb in range(2):
+            skip = f".Lw64_skip_{tag}{qb}_%="
+            blk += [f"s_cmp_lg_u32 s{S_VCC + qb}, 0", f"s_cbranch_scc0 {skip}"]
+            blk += self.slow_block(p, qb, f"{tag}{qb}")
+            blk += [f"{skip}:"]
+        blk += ["s_nop 7", f"s_branch {back}"]
+        self.slow.append(blk)
+
+    def slow_block(self, p, qb, tag):
+        """Exact row max of S[p][qb], O / sum rescale when it moved by more
+        than 8, all 32 weights again (update_max and the slow path of
+        soft_pv in kd_fa_kernel.hip)."""
+        tr = Tracker()
+        sb = S_BASE[p] + 32 * qb
+        w = [W_BASE + i for i in range(7)]
+        s = [vr(sb + i) for i in range(32)]
+        e = tr.emit
+        e(valu(f"v_max3_f32 {vr(w[0])}, {s[0]}, {s[1]}, {s[2]}", set(s[0:3]), {vr(w[0])}))
+        e(valu(f"v_max3_f32 {vr(w[1])}, {s[3]}, {s[4]}, {s[5]}", set(s[3:6]), {vr(w[1])}))
+        for i in range(6, 30, 4):
+            e(valu(f"v_max3_f32 {vr(w[0])}, {vr(w[0])}, {s[i]}, {s[i + 1]}", {vr(w[0]), s[i], s[i + 1]}, {vr(w[0])}))
+            e(valu(f"v_max3_f32 {vr(w[1])}, {vr(w[1])}, {s[i + 2]}, {s[i + 3]}", {vr(w[1]), s[i + 2], s[i + 3]},
+                   {vr(w[1])}))
+        e(valu(f"v_max_f32 {vr(w[2])}, {s[30]}, {s[31]}", {s[30], s[31]}, {vr(w[2])}))
+        e(valu(f"v_max3_f32 {vr(w[0])}, {vr(w[0])}, {vr(w[1])}, {vr(w[2])}", {vr(w[0]), vr(w[1]), vr(w[2])},
+               {vr(w[0])}))
+        # max over the lane pair, times |c2|
+        e(valu(f"v_mov_b32 {vr(X)}, {vr(w[0])}", {vr(w[0])}, {vr(X)}))
+        e(valu(f"v_mov_b32 {vr(Y)}, {vr(w[0])}", {vr(w[0])}, {vr(Y)}))
+        e(Ins(f"v_permlane32_swap_b32 {vr(X)}, {vr(Y)}", "perm", {vr(X), vr(Y)}, {vr(X), vr(Y)}))
+        e(valu(f"v_max_f32 {vr(X)}, {vr(X)}, {vr(Y)}", {vr(X), vr(Y)}, {vr(X)}))
+        e(valu(f"v_mul_f32 {vr(X)}, |%[c2]|, {vr(X)}", {vr(X)}, {vr(X)}))
+        # update when some row's max exceeds its running max by more than 8
+        e(valu(f"v_add_f32 {vr(Y)}, 0x41000000, {vr(M[qb])}", {vr(M[qb])}, {vr(Y)}))
+        e(valu(f"v_cmp_gt_f32 vcc, {vr(X)}, {vr(Y)}", {vr(X), vr(Y)}, ()))
+        noupd = f".Lw64_noupd_{tag}_%="
+        e(Ins(f"s_cbranch_vccz {noupd}", "branch"))
+        e(valu(f"v_max_f32 {vr(Y)}, {vr(M[qb])}, {vr(X)}", {vr(M[qb]), vr(X)}, {vr(Y)}))        # m_new
+        e(valu(f"v_sub_f32 {vr(w[2])}, {vr(M[qb])}, {vr(Y)}", {vr(M[qb]), vr(Y)}, {vr(w[2])}))
+        e(Ins(f"v_exp_f32 {vr(w[2])}, {vr(w[2])}", "trans", {vr(w[2])}, {vr(w[2])}))
+        e(valu(f"v_cmp_neq_f32 vcc, {vr(Y)}, {vr(M[qb])}", {vr(Y), vr(M[qb])}, ()))
+        e(valu(f"v_cndmask_b32 {vr(w[2])}, 1.0, {vr(w[2])}, vcc", {vr(w[2])}, {vr(w[2])}))          # alpha
+        e(valu(f"v_mov_b32 {vr(M[qb])}, {vr(Y)}", {vr(Y)}, {vr(M[qb])}))
+        e(valu(f"v_mul_f32 {vr(LH[qb])}, {vr(LH[qb])}, {vr(w[2])}", {vr(LH[qb]), vr(w[2])}, {vr(LH[qb])}))
+        tmp = w[3:7]
+        for c in range(0, 64, 4):
+            for i in range(4):
+                a = f"a{A_O + 64 * qb + c + i}"
+                e(Ins(f"v_accvgpr_read_b32 {vr(tmp[i])}, {a}", "valu", {a}, {vr(tmp[i])}))
+            for i in range(4):
+                e(valu(f"v_mul_f32 {vr(tmp[i])}, {vr(tmp[i])}, {vr(w[2])}", {vr(tmp[i]), vr(w[2])}, {vr(tmp[i])}))
+            for i in range(4):
+                a = f"a{A_O + 64 * qb + c + i}"
+                e(Ins(f"v_accvgpr_write_b32 {a}, {vr(tmp[i])}", "accw", {vr(tmp[i])}, {a}))
+        tr.label(noupd)
+        for x in self.softmax_half(p, p, 0, (qb,), True) + self.softmax_half(p, p, 1, (qb,), True):
+            e(x)
+        return tr.out
+
+    # -------------------------------------------------------------- step
+    def step(self, tr, p, final, tag):
+        """Step t with parity p: S(t) in S[p], K(t+1) in KBUF[1-p], V(t) in
+        VBUF[p]; P[p] holds the weights of keys 0-31 of tile t."""
+        q = 1 - p
+        if not final:
+            pre, seq = self.qk_stream(KBUF[q], q)
+            for r in pre:
+                tr.emit(r)
+            dmas = [self.dma("v", VBUF[q], j) for j in range(4)] + [self.advance("v")] + \
+                   [self.dma("k", KBUF[p], j) for j in range(4)] + [self.advance("k")]
+            self.merge(tr, seq, self.softmax_half(p, p, 1, (0, 1), True), dmas)
+        else:
+            for x in self.softmax_half(p, p, 1, (0, 1), True):
+                tr.emit(x)
+        vpre, vseq = self.pv_stream(VBUF[p], p)
+        for r in vpre:
+            tr.emit(r)
+        self.check(tr, p, tag)
+        if not final:
+            self.merge(tr, vseq, self.softmax_half(q, q, 0, (0, 1), True))
+            tr.raw("s_waitcnt vmcnt(0)")
+            tr.raw("s_barrier")
+            tr.settle()
+        else:
+            self.merge(tr, vseq, [])
+
+    def build(self):
+        tr = Tracker()
+        e = tr.emit
+        e(valu(f"v_mov_b32 {vr(ONE)}, {self.one}", (), {vr(ONE)}))
+        for qb in range(2):
+            e(valu(f"v_mov_b32 {vr(M[qb])}, 0xff800000", (), {vr(M[qb])}))
+            e(valu(f"v_mov_b32 {vr(LH[qb])}, 0", (), {vr(LH[qb])}))
+        for i in range(128):
+            e(Ins(f"v_accvgpr_write_b32 a{A_O + i}, 0", "accw", (), {f"a{A_O + i}"}))
+        for i in range(16):
+            e(Ins(f"ds_read_b128 {arng(A_Q + 4 * i, 4)}, %[qrd] offset:{1024 * i}", "lds_rd", (), aset(A_Q + 4 * i, 4)))
+        for j, w in enumerate(("kw0", "kw1", "kw2", "kw3")):
+            e(Ins(f"s_mov_b32 s{S_K + j}, %[{w}]", "salu"))
+        for j, w in enumerate(("vw0", "vw1", "vw2", "vw3")):
+            e(Ins(f"s_mov_b32 s{S_V + j}, %[{w}]", "salu"))
+        # K(0), V(0), K(1) (a DMA past the last tile reads zeros: the
+        # resource's record count is clamped at 0)
+        for j in range(4):
+            for x in self.dma("k", KBUF[0], j):
+                e(x)
+        for x in self.advance("k"):
+            e(x)
+        for j in range(4):
+            for x in self.dma("v", VBUF[0], j):
+                e(x)
+        for x in self.advance("v"):
+            e(x)
+        for j in range(4):
+            for x in self.dma("k", KBUF[1], j):
+                e(x)
+        for x in self.advance("k"):
+            e(x)
+        tr.raw("s_waitcnt vmcnt(0) lgkmcnt(0)")
+        tr.lds = []
+        tr.raw("s_barrier")
+        # S(0), then every wave is done with K(0) before K(2) lands there
+        pre, seq = self.qk_stream(KBUF[0], 0)
+        for r in pre:
+            e(r)
+        self.merge(tr, seq, [])
+        tr.raw("s_barrier")
+        for x in self.softmax_half(0, 0, 0, (0, 1), True):
+            e(x)
+        # steps: pairs while t + 2 < n, then one or two more
+        tr.raw(f"s_mov_b32 s{S_T}, 0")
+        tr.label(".Lw64_loop_%=")
+        tr.raw(f"s_add_u32 s{S_TMP}, s{S_T}, 2")
+        tr.raw(f"s_cmp_lt_u32 s{S_TMP}, %[n]")
+        tr.raw(".Lw64_tail_%=".join(["s_cbranch_scc0 ", ""]))
+        self.step(tr, 0, False, "a")
+        self.step(tr, 1, False, "b")
+        tr.raw(f"s_add_u32 s{S_T}, s{S_T}, 2")
+        tr.raw("s_branch .Lw64_loop_%=")
+        tr.label(".Lw64_tail_%=")
+        tr.raw(f"s_add_u32 s{S_TMP}, s{S_T}, 1")
+        tr.raw(f"s_cmp_lt_u32 s{S_TMP}, %[n]")
+        tr.raw("s_cbranch_scc0 .Lw64_last0_%=")
+        self.step(tr, 0, False, "c")
+        self.step(tr, 1, True, "d")
+        tr.raw("s_branch .Lw64_done_%=")
+        tr.label(".Lw64_last0_%=")
+        self.step(tr, 0, True, "e")
+        tr.label(".Lw64_done_%=")
+        # O and the sums -> LDS (over K, V and Q, once every wave is done)
+        tr.raw("s_nop 7", 8)
+        tr.raw("s_nop 7", 8)
+        tr.raw("s_nop 7", 8)
+        tr.raw("s_barrier")
+        tr.mfma_w.clear()
+        for qb in range(2):
+            for dblk in range(4):
+                for g in range(4):
+                    a = A_O + 64 * qb + 16 * dblk + 4 * g
+                    e(Ins(f"ds_write_b128 %[ord], {arng(a, 4)} offset:{((qb * 4 + dblk) * 4 + g) * 1024}", "lds_wr",
+                          aset(a, 4), ()))
+        for qb in range(2):
+            e(Ins(f"ds_write_b32 %[lrd], {vr(LH[qb])} offset:{256 * qb}", "lds_wr", {vr(LH[qb])}, ()))
+        tr.raw("s_waitcnt lgkmcnt(0)")
+        tr.raw("s_branch .Lw64_end_%=")
+        lines = tr.out
+        for blk in self.slow:
+            lines += blk
+        lines.append(".Lw64_end_%=:")
+        return lines
+
+
+def check_registers(lines):
+    """Every register named is inside the loop's ranges or an operand."""
+    for ln in lines:
+        for m in re.finditer(r"\b([va])\[(\d+):(\d+)\]|\b([va])(\d+)\b", ln):
+            if m.group(1):
+                kind, lo, hi = m.group(1), int(m.group(2)), int(m.group(3))
+            else:
+                kind, lo, hi = m.group(4), int(m.group(5)), int(m.group(5))
+            if kind == "v":
+                assert 24 <= lo and hi <= V_LAST, ln
+            else:
+                assert 0 <= lo and hi <= A_LAST, ln
+        for m in re.finditer(r"\bs\[?(\d+)", ln):
+            assert S_FIRST <= int(m.group(1)) <= S_LAST + 3, ln
+
+
+def main(path=None):
+    here = os.path.dirname(os.path.abspath(__file__))
+    path = path or os.path.join(here, "kd_fa_w64_loop.inc")
+    out = ["// Generated by gen_w64_loop.py from this directory; do not edit.",
+           "// The key loop of fa_fwd_w64 (kd_fa_kernel.hip) as inline-asm text.", ""]
+    for T in ("bf16", "f16"):
+        lines = Gen(T).build()
+        check_registers(lines)
+        out.append(f"#define KD_W64_LOOP_{T.upper()} \\")
+        for ln in lines:
+            out.append(f'    "{ln}\\n" \\')
+        out.append('    ""')
+        out.append("")
+    out.append("#define KD_W64_CLOBBERS \\")
+    regs = [f'"v{i}"' for i in range(24, V_LAST + 1)] + [f'"a{i}"' for i in range(A_LAST + 1)] + \
+           [f'"s{i}"' for i in range(S_FIRST, S_LAST + 1)]
+    for k in range(0, len(regs), 16):
+        out.append("    " + ", ".join(regs[k:k + 16]) + ", \\")
+    out.append('    "vcc", "scc", "m0", "memory"')
+    with open(path, "w") as f:
+        f.write("\n".join(out) + "\n")
+
+
+if __name__ == "__main__":
+    import sys
+    main(sys.argv[1] if len(sys.argv) > 1 else None)

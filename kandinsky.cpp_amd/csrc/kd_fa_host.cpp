@@ -6,6 +6,7 @@
 
 #include <atomic>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -138,6 +139,18 @@ size_t rope_ws_bytes(const kd_fa_desc *d) {
 // RoPE mode asks for it: with ws != nullptr once into ws (contiguous, K's
 // type), after which the attention transforms only Q on load; without, by
 // the attention kernel on every K tile it loads.
+
+// The 64-rows-per-wave kernel takes the unmasked calls whose K streams from
+// memory as stored (no transform on load) and whose keys fill whole 64-key
+// tiles; its buffer-resource offsets are 32-bit.  KD_FA_W64=0 in the
+// environment routes every call to the 32-row kernel (for comparisons).
+static bool use_w64(const kdfa::Args &a, bool k_on_load) {
+    const char *e = std::getenv("KD_FA_W64");
+    if ((e && e[0] == '0') || a.m || k_on_load || a.Lk < 64 || a.Lk % 64 != 0) return false;
+    const int64_t lim = (int64_t)1 << 31;
+    return (int64_t)(a.Lk - 1) * a.k_nb1 + 256 < lim && (int64_t)(a.Lk - 1) * a.v_nb1 + 256 < lim;
+}
+
 int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *ws, size_t ws_bytes,
         void *stream) {
     bool mask_vec = false;
@@ -214,7 +227,9 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
         a.k_nb2 = row * a.Lk;
         a.k_nb3 = row * a.Lk * hk;
     }
-    if (kdfa::launch(a, d->v.type, k_rope, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
+    const hipError_t e = use_w64(a, k_rope) ? kdfa::launch_w64(a, d->v.type, hs)
+                                            : kdfa::launch(a, d->v.type, k_rope, hs);
+    if (e != hipSuccess) return KD_FA_ERR_LAUNCH;
     return KD_FA_OK;
 }
 

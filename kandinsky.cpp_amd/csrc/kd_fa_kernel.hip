@@ -50,6 +50,34 @@ template <int PRE> __device__ __forceinline__ void sched_qk() {
     sched_qk_step<4, PRE>(); sched_qk_step<5, PRE>(); sched_qk_step<6, PRE>(); sched_qk_step<7, PRE>();
 }
 
+// Instruction order of the pipelined step's first half: the S^T product of
+// the next tile (16 MFMA, 16 K-fragment reads) with the softmax of the
+// current tile spread between its MFMAs, VPM VALU instructions after each.
+// (0x402: VALU or transcendental.)
+template <int KS, int PRE, int VPM> __device__ __forceinline__ void sched_pipe_step() {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x402, VPM, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x402, VPM, 0);
+    if constexpr (KS + PRE < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+}
+template <int PRE, int VPM> __device__ __forceinline__ void sched_pipe() {
+    for (int i = 0; i < PRE; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    sched_pipe_step<0, PRE, VPM>(); sched_pipe_step<1, PRE, VPM>(); sched_pipe_step<2, PRE, VPM>();
+    sched_pipe_step<3, PRE, VPM>(); sched_pipe_step<4, PRE, VPM>(); sched_pipe_step<5, PRE, VPM>();
+    sched_pipe_step<6, PRE, VPM>(); sched_pipe_step<7, PRE, VPM>();
+}
+
+// Software-pipelined key loop for the kernels that stream K by DMA (no
+// mask): the S^T product of tile t+1 is interleaved with the softmax of
+// tile t in the same wave (tuning switch; 0 = one phase after the other).
+#ifndef KD_FA_PIPE
+#define KD_FA_PIPE 1
+#endif
+#ifndef KD_FA_PIPE_VPM
+#define KD_FA_PIPE_VPM 6
+#endif
+
 // Wave priority around the MFMA sections (tuning switch).
 #ifndef KD_FA_SETPRIO
 #define KD_FA_SETPRIO 0
@@ -74,6 +102,81 @@ template <int PRE> __device__ __forceinline__ void sched_qk() {
 #else
 #define KD_FA_PRIO(x) ((void)0)
 #endif
+
+// Q fragments of query row q_ld (B operands of S^T = K Q^T, k-steps of 16):
+// this lane holds elements ks*16 + hi*8 .. +7 of each k-step; the lane
+// l ^ 32 the other half.  RMSNorm (qn_w) and RoPE (RM) are applied in F32
+// first; scale < 0 negates Q (exact) so that every score is s * |scale|.
+template <typename T, int RM>
+__device__ __forceinline__ void load_q_frags(const Args &a, int q_ld, int h, int b, int hi,
+                                             typename Elem<T>::vec8 qf[8]) {
+    typedef Elem<T> E;
+    typedef typename E::vec8 vec8;
+    constexpr bool ROPE = RM != KD_FA_ROPE_NONE;
+    const char *qp = a.q + (int64_t)q_ld * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)b * a.q_nb3;
+    const int esz = a.q_type == KD_FA_TYPE_F32 ? 4 : 2;
+    // RMSNorm of the row (query_norm): this lane holds 64 of its 128
+    // elements, the lane l ^ 32 the rest
+    float qscale = 1.0f;
+    if (a.qn_w) {
+        double ss = 0.0;
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            float x[8];
+            load8_f32(qp + (ks * 16 + hi * 8) * esz, a.q_type, x);
+            ss += sum_sq8(x);
+        }
+        qscale = rms_scale(pair_sum_f64(ss), a.norm_eps);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+        const int d0 = ks * 16 + hi * 8;
+        float x[8];
+        load8_f32(qp + d0 * esz, a.q_type, x);
+        if (a.qn_w)
+            rms_apply8(x, qscale, *reinterpret_cast<const f32x4 *>(a.qn_w + d0),
+                       *reinterpret_cast<const f32x4 *>(a.qn_w + d0 + 4));
+        if (ROPE) {
+            const float *cp = rope_ptr<RM>(a, q_ld, d0);
+            rotate8(x, *reinterpret_cast<const f32x4 *>(cp), *reinterpret_cast<const f32x4 *>(cp + 4));
+        }
+        u32x4 w;
+        for (int j = 0; j < 4; ++j) w[j] = E::pack2(x[2 * j], x[2 * j + 1]);
+        if (a.scale_log2 < 0.0f) w ^= (u32x4){0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
+        qf[ks] = __builtin_bit_cast(vec8, w);
+    }
+}
+
+// O / l of query row q_row -> dst[b][q_row][h][:] (F32, or rounded to
+// F16 / BF16).  o holds O^T of the row's 32-row block in MFMA accumulator
+// order (element i of d block dblk: d = dblk*32 + 8*(i/4) + 4*hi + i%4);
+// l_half is this lane's half of the row's weight sum.
+__device__ __forceinline__ void store_o_row(const Args &a, int q_row, int h, int b, int hi, const f32x16 o[4],
+                                            float l_half) {
+    const float l_run = pair_sum(l_half);
+    if (q_row < a.Lq) {
+        const float inv = l_run == 0.0f ? 0.0f : 1.0f / l_run;
+        char *op = a.o + (int64_t)b * a.o_nb3 + (int64_t)q_row * a.o_nb2 + (int64_t)h * a.o_nb1;
+        const int ot = a.o_type;
+#pragma unroll
+        for (int dblk = 0; dblk < 4; ++dblk)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = dblk * 32 + 8 * g + 4 * hi;
+                const f32x4 v = {o[dblk][4 * g] * inv, o[dblk][4 * g + 1] * inv,
+                                 o[dblk][4 * g + 2] * inv, o[dblk][4 * g + 3] * inv};
+                if (ot == KD_FA_TYPE_F32) {
+                    *reinterpret_cast<f32x4 *>(op + d * 4) = v;
+                } else if (ot == KD_FA_TYPE_BF16) {
+                    const u32x2 w = {Elem<__bf16>::pack2(v.x, v.y), Elem<__bf16>::pack2(v.z, v.w)};
+                    *reinterpret_cast<u32x2 *>(op + d * 2) = w;
+                } else {
+                    const u32x2 w = {Elem<_Float16>::pack2(v.x, v.y), Elem<_Float16>::pack2(v.z, v.w)};
+                    *reinterpret_cast<u32x2 *>(op + d * 2) = w;
+                }
+            }
+    }
+}
 
 template <typename T, bool HAS_MASK, int RM, bool KROPE>
 __global__ __launch_bounds__(64 * waves_per_block(HAS_MASK, KROPE)) __attribute__((amdgpu_waves_per_eu(2)))
@@ -132,42 +235,7 @@ void fa_fwd_d128(Args a) {
     const int q_row = qt * kBM + wave * 32 + l32;
     const int q_ld = q_row < a.Lq ? q_row : a.Lq - 1;
     vec8 qf[8];
-    {
-        const char *qp = a.q + (int64_t)q_ld * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)b * a.q_nb3;
-        const int esz = a.q_type == KD_FA_TYPE_F32 ? 4 : 2;
-        // RMSNorm of the row (query_norm): this lane holds 64 of its 128
-        // elements, the lane l ^ 32 the rest
-        float qscale = 1.0f;
-        if (a.qn_w) {
-            double ss = 0.0;
-#pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
-                float x[8];
-                load8_f32(qp + (ks * 16 + hi * 8) * esz, a.q_type, x);
-                ss += sum_sq8(x);
-            }
-            qscale = rms_scale(pair_sum_f64(ss), a.norm_eps);
-        }
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-            const int d0 = ks * 16 + hi * 8;
-            float x[8];
-            load8_f32(qp + d0 * esz, a.q_type, x);
-            if (a.qn_w)
-                rms_apply8(x, qscale, *reinterpret_cast<const f32x4 *>(a.qn_w + d0),
-                           *reinterpret_cast<const f32x4 *>(a.qn_w + d0 + 4));
-            if (ROPE) {
-                const float *cp = rope_ptr<RM>(a, q_ld, d0);
-                rotate8(x, *reinterpret_cast<const f32x4 *>(cp), *reinterpret_cast<const f32x4 *>(cp + 4));
-            }
-            u32x4 w;
-            for (int j = 0; j < 4; ++j) w[j] = E::pack2(x[2 * j], x[2 * j + 1]);
-            // scale < 0: use -q (exact) and |scale|, so that every score
-            // below is s * c2 with c2 >= 0 and its max is max(s) * c2
-            if (a.scale_log2 < 0.0f) w ^= (u32x4){0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
-            qf[ks] = __builtin_bit_cast(vec8, w);
-        }
-    }
+    load_q_frags<T, RM>(a, q_ld, h, b, hi, qf);
 
     const uint16_t *mrow = nullptr;
     if (HAS_MASK) {
@@ -373,18 +441,21 @@ void fa_fwd_d128(Args a) {
 
     // P rounded to the operand type (the PV B operands); the row sum uses
     // the same rounded weights as the numerator
+    // the sum of each 16-key step is its own dot2 chain (short dependency
+    // chains), the four combined as (s0 + s1) + (s2 + s3)
     auto pack_sum = [&](const float *p, vec8 pb[4]) -> float {
-        float sum = 0.0f;
+        float part[4];
 #pragma unroll
         for (int kst = 0; kst < 4; ++kst) {
             u32x4 w;
+            part[kst] = 0.0f;
             for (int j = 0; j < 4; ++j) {
                 w[j] = E::pack2(p[8 * kst + 2 * j], p[8 * kst + 2 * j + 1]);
-                sum = E::sum2(w[j], sum);
+                part[kst] = E::sum2(w[j], part[kst]);
             }
             pb[kst] = __builtin_bit_cast(vec8, w);
         }
-        return sum;
+        return (part[0] + part[1]) + (part[2] + part[3]);
     };
     auto pack_p = [&](const float *p, vec8 pb[4]) __attribute__((always_inline)) { l_half += pack_sum(p, pb); };
 
@@ -485,7 +556,118 @@ void fa_fwd_d128(Args a) {
         KD_FA_PRIO(0);
     };
 
-    if constexpr (!HAS_MASK) {
+    if constexpr (!HAS_MASK && !KR && KD_FA_PIPE) {
+        // Pipelined: while step t computes the softmax of tile t, the same
+        // wave issues the S^T products of tile t+1 between its VALU
+        // instructions; the PV products of tile t follow.  K is staged one
+        // tile ahead of V: during step t the LDS holds K(t+1) and V(t), and
+        // the DMA fills K(t+2) (into the buffer K(t) left) and V(t+1).
+        if (n_tiles > 0) {
+            issue_k(0, sK0);
+            issue_v(0, sV0);
+            if (n_tiles > 1) issue_k(1, sK1);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        f32x16 sa0, sa1, sb0, sb1;
+        if (n_tiles > 0) qk(sK0, sa0, sa1);
+        __syncthreads();   // every wave is done with K(0) before K(2) lands in its buffer
+        // c0, c1: scores of tile t; n0, n1 <- scores of tile t+1 (NEXT)
+        auto pstep = [&](auto next_c, auto tail_c, int t, const f32x16 &c0, const f32x16 &c1, f32x16 &n0,
+                         f32x16 &n1, const lds_t *kn_, const lds_t *vs_, lds_t *dK, lds_t *dV)
+                         __attribute__((always_inline)) {
+            constexpr bool NEXT = decltype(next_c)::value;
+            constexpr bool TAIL = decltype(tail_c)::value;
+            constexpr int kKPre = KD_FA_KPRE;
+            if (NEXT) {
+                issue_v(t + 1, dV);
+                if (t + 2 < n_tiles) issue_k(t + 2, dK);
+            }
+            const int key0 = t * kBN;
+            auto drop_tail = [&](float *p) __attribute__((always_inline)) {
+                if (TAIL) {
+#pragma unroll
+                    for (int i = 0; i < 32; ++i) {
+                        const int key = key0 + (i >> 4) * 32 + 16 * ((i >> 3) & 1) + 8 * hi + (i & 7);
+                        p[i] = key < Lk ? p[i] : 0.0f;
+                    }
+                }
+            };
+            vec8 pb[4];
+            float p[32];
+            float nm = -m_run;
+            vec8 ka[8][2];
+            if (NEXT) {
+                n0 = (f32x16){};
+                n1 = (f32x16){};
+#pragma unroll
+                for (int ks = 0; ks < kKPre; ++ks) {
+                    ka[ks][0] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(kn_ + k_rd[ks]);
+                    ka[ks][1] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(kn_ + k_rd[ks] + 32 * 256);
+                }
+#pragma unroll
+                for (int ks = 0; ks < 8; ++ks) {
+                    if (ks + kKPre < 8) {
+                        ka[ks + kKPre][0] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(kn_ + k_rd[ks + kKPre]);
+                        ka[ks + kKPre][1] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(kn_ + k_rd[ks + kKPre] + 32 * 256);
+                    }
+                    n0 = E::mfma(ka[ks][0], qf[ks], n0);
+                    n1 = E::mfma(ka[ks][1], qf[ks], n1);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(c0[i], c2, nm));
+                p[16 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(c1[i], c2, nm));
+            }
+            drop_tail(p);
+            float sum = pack_sum(p, pb);
+            if (NEXT) sched_pipe<kKPre, KD_FA_PIPE_VPM>();
+            const float pair = pair_sum(sum);
+            // the weight sum left [0, 2^kSumCap]: exact max, rescale, redo
+            if (__builtin_amdgcn_ballot_w64(!(pair <= kSumCap)) != 0) {
+                float q[32];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) { q[i] = c0[i]; q[16 + i] = c1[i]; }
+                update_max(pair_max(max32(q)) * c2);
+                nm = -m_run;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(c0[i], c2, nm));
+                    p[16 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(c1[i], c2, nm));
+                }
+                drop_tail(p);
+                sum = pack_sum(p, pb);
+            }
+            l_half += sum;
+            pv(vs_, pb);
+            if (NEXT) {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __syncthreads();
+            }
+        };
+        // steps 0 .. n_tiles-2 have a next tile (and are full tiles); the
+        // last step may be partial.  Step t: K(t+1) in sK[(t+1)&1], V(t) in
+        // sV[t&1].
+        int t = 0;
+        for (; t + 2 < n_tiles; t += 2) {
+            pstep(BC<true>(), BC<false>(), t, sa0, sa1, sb0, sb1, sK1, sV0, sK0, sV1);
+            pstep(BC<true>(), BC<false>(), t + 1, sb0, sb1, sa0, sa1, sK0, sV1, sK1, sV0);
+        }
+        const bool tail = Lk % kBN != 0;
+        if (t + 1 < n_tiles) {   // two steps left: t (even) and t+1 (last)
+            pstep(BC<true>(), BC<false>(), t, sa0, sa1, sb0, sb1, sK1, sV0, sK0, sV1);
+            if (tail)
+                pstep(BC<false>(), BC<true>(), t + 1, sb0, sb1, sa0, sa1, sK0, sV1, sK1, sV0);
+            else
+                pstep(BC<false>(), BC<false>(), t + 1, sb0, sb1, sa0, sa1, sK0, sV1, sK1, sV0);
+        } else if (t < n_tiles) {   // one step left: t (even, last)
+            if (tail)
+                pstep(BC<false>(), BC<true>(), t, sa0, sa1, sb0, sb1, sK1, sV0, sK0, sV1);
+            else
+                pstep(BC<false>(), BC<false>(), t, sa0, sa1, sb0, sb1, sK1, sV0, sK0, sV1);
+        }
+    } else if constexpr (!HAS_MASK) {
         // Two LDS stages; tile t+1 streams in while tile t is computed.
         if (n_tiles > 0) load_tile_sync(0, sK0, sV0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -564,29 +746,172 @@ void fa_fwd_d128(Args a) {
     }
 
     // ---- epilogue: O / l -> dst[b][q][h][:] (F32, or rounded to F16 / BF16) --
-    const float l_run = pair_sum(l_half);
-    if (q_row < a.Lq) {
-        const float inv = l_run == 0.0f ? 0.0f : 1.0f / l_run;
-        char *op = a.o + (int64_t)b * a.o_nb3 + (int64_t)q_row * a.o_nb2 + (int64_t)h * a.o_nb1;
-        const int ot = a.o_type;
+    store_o_row(a, q_row, h, b, hi, o, l_half);
+}
+
+// ---------------------------------------------------------------------------
+// fa_fwd_w64: the unmasked kernel with 64 query rows per wave.
+//
+// One workgroup = 4 waves = 256 query rows of one (batch, head), one wave per
+// SIMD with 512 registers: O^T (128 floats per lane) and the Q fragments
+// (64) stay in AGPRs as MFMA operands.  A K or V^T fragment read from LDS
+// now feeds two MFMAs (one per 32-row block), which halves the LDS operand
+// traffic per flop of fa_fwd_d128, and the softmax of one tile runs between
+// the matrix products of the next tile in the same wave.  The key loop is
+// hand-scheduled ISA (kd_fa_w64_loop.inc, written by gen_w64_loop.py);
+// its arithmetic is fa_fwd_d128's step for step, so that both kernels give
+// bitwise identical results.  K and V stream global -> LDS through buffer
+// resources whose record count stops at the last key (a DMA past it reads
+// zeros).  Lk is a positive multiple of 64 (no partial tile).
+// LDS: K and V tiles double-buffered (0 .. 64 KiB), the Q fragments handed
+// to the loop (64 .. 128 KiB); after the loop, O (0 .. 128 KiB) and the row
+// sums (128 .. 130 KiB) handed back.
+#include "kd_fa_w64_loop.inc"
+
+constexpr int kW64Lds = 133120;
+constexpr int kW64QOff = 65536;
+constexpr int kW64LOff = 131072;
+
+template <typename T, int RM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void fa_fwd_w64(Args a) {
+    typedef Elem<T> E;
+    typedef typename E::vec8 vec8;
+    __shared__ __attribute__((aligned(1024))) char lds_arr[kW64Lds];
+    lds_t *const lds = LDS_PTR(char, lds_arr);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31;
+    const int hi = lane >> 5;
+
+    // block order as in fa_fwd_d128 (unmasked: the q-tiles of one head in a
+    // row, each XCD a contiguous range)
+    const int pid = blockIdx.x;
+    const int per = a.n_blocks >> 3;
+    const int lid = pid < per * 8 ? (pid & 7) * per + (pid >> 3) : pid;
+    const int qt = lid % a.n_qt;
+    const int bh = lid / a.n_qt;
+    const int h = bh % a.H;
+    const int b = bh / a.H;
+
+    // Q fragments of the wave's two 32-row blocks -> LDS, lane-major
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        const int q_row = qt * 256 + wave * 64 + qb * 32 + l32;
+        const int q_ld = q_row < a.Lq ? q_row : a.Lq - 1;
+        vec8 qf[8];
+        load_q_frags<T, RM>(a, q_ld, h, b, hi, qf);
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks)
+            *reinterpret_cast<__attribute__((address_space(3))) vec8 *>(
+                lds + kW64QOff + wave * 16384 + (qb * 8 + ks) * 1024 + lane * 16) = qf[ks];
+    }
+
+    // per-lane LDS offsets of the operand reads (fa_fwd_d128's k_rd / v_rd)
+    uint32_t krd[8], vrd[4];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) krd[ks] = lds0 + l32 * 256 + (((2 * ks + hi) ^ (lane & 15)) << 4);
+    const int v_sub = (lane & 15) >> 2;
+    const int v_c_lo = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+#pragma unroll
+    for (int dblk = 0; dblk < 4; ++dblk)
+        vrd[dblk] = lds0 + 2048 * hi + 256 * v_sub + (((4 * dblk + v_c_lo) ^ v_swz(v_sub)) << 4) + 8 * (lane & 1);
+    // DMA: round j of wave w fills tile rows 4*(w + 4j) .. +3 (1 KiB at
+    // LDS (w + 4j) * 1024); lane: row 4*(w + 4j) + lane/16, chunk lane%16
+    const int r0 = 4 * wave + (lane >> 4);
+    const int pc = lane & 15;
+    uint32_t kdma[4], vdma[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        kdma[j] = (uint32_t)(k_row_of(r0) + 16 * j) * (uint32_t)a.k_nb1 + ((pc ^ (r0 & 15)) << 4);
+        vdma[j] = (uint32_t)(r0 + 16 * j) * (uint32_t)a.v_nb1 + ((pc ^ v_swz(r0)) << 4);
+    }
+    const uint32_t qrd = lds0 + kW64QOff + wave * 16384 + lane * 16;
+    const uint32_t ord = lds0 + wave * 32768 + lane * 16;
+    const uint32_t lrd = lds0 + kW64LOff + wave * 512 + lane * 4;
+    const uint32_t dmab = __builtin_amdgcn_readfirstlane(lds0 + wave * 1024);
+
+    // buffer resources of this head's K and V: base, no stride, records up to
+    // the end of key Lk-1, raw dword access
+    const char *kbase = a.k + (int64_t)(h / a.rk2) * a.k_nb2 + (int64_t)(b / a.rk3) * a.k_nb3;
+    const char *vbase = a.v + (int64_t)(h / a.rv2) * a.v_nb2 + (int64_t)(b / a.rv3) * a.v_nb3;
+    const uint64_t ka = (uint64_t)(uintptr_t)kbase, va = (uint64_t)(uintptr_t)vbase;
+    const uint32_t kw0 = __builtin_amdgcn_readfirstlane((uint32_t)ka);
+    const uint32_t kw1 = __builtin_amdgcn_readfirstlane((uint32_t)(ka >> 32) & 0xffffu);
+    const uint32_t kw2 = __builtin_amdgcn_readfirstlane((uint32_t)(a.Lk - 1) * (uint32_t)a.k_nb1 + 256u);
+    const uint32_t vw0 = __builtin_amdgcn_readfirstlane((uint32_t)va);
+    const uint32_t vw1 = __builtin_amdgcn_readfirstlane((uint32_t)(va >> 32) & 0xffffu);
+    const uint32_t vw2 = __builtin_amdgcn_readfirstlane((uint32_t)(a.Lk - 1) * (uint32_t)a.v_nb1 + 256u);
+    const uint32_t rw3 = 0x00020000u;
+    const uint32_t ktile = __builtin_amdgcn_readfirstlane(64u * (uint32_t)a.k_nb1);
+    const uint32_t vtile = __builtin_amdgcn_readfirstlane(64u * (uint32_t)a.v_nb1);
+    const uint32_t n_tiles = __builtin_amdgcn_readfirstlane((uint32_t)(a.Lk / kBN));
+    const float c2 = __builtin_fabsf(a.scale_log2);
+
+    __syncthreads();
+#define KD_W64_OPERANDS                                                                              \
+    [krd0] "v"(krd[0]), [krd1] "v"(krd[1]), [krd2] "v"(krd[2]), [krd3] "v"(krd[3]), [krd4] "v"(krd[4]), \
+        [krd5] "v"(krd[5]), [krd6] "v"(krd[6]), [krd7] "v"(krd[7]), [vrd0] "v"(vrd[0]), [vrd1] "v"(vrd[1]), \
+        [vrd2] "v"(vrd[2]), [vrd3] "v"(vrd[3]), [kdma0] "v"(kdma[0]), [kdma1] "v"(kdma[1]),                \
+        [kdma2] "v"(kdma[2]), [kdma3] "v"(kdma[3]), [vdma0] "v"(vdma[0]), [vdma1] "v"(vdma[1]),            \
+        [vdma2] "v"(vdma[2]), [vdma3] "v"(vdma[3]), [qrd] "v"(qrd), [ord] "v"(ord), [lrd] "v"(lrd),        \
+        [kw0] "s"(kw0), [kw1] "s"(kw1), [kw2] "s"(kw2), [kw3] "s"(rw3), [vw0] "s"(vw0), [vw1] "s"(vw1),    \
+        [vw2] "s"(vw2), [vw3] "s"(rw3), [ktile] "s"(ktile), [vtile] "s"(vtile), [n] "s"(n_tiles),          \
+        [c2] "s"(c2), [dmab] "s"(dmab)
+// (m0 is in the clobber list for the reader; the compiler reserves it and
+// uses it nowhere in this kernel)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+    if constexpr (__is_same(T, __bf16))
+        asm volatile(KD_W64_LOOP_BF16 : : KD_W64_OPERANDS : KD_W64_CLOBBERS);
+    else
+        asm volatile(KD_W64_LOOP_F16 : : KD_W64_OPERANDS : KD_W64_CLOBBERS);
+#pragma clang diagnostic pop
+#undef KD_W64_OPERANDS
+    __syncthreads();
+
+    // O and the half-row sums from LDS -> dst
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        f32x16 o[4];
 #pragma unroll
         for (int dblk = 0; dblk < 4; ++dblk)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int d = dblk * 32 + 8 * g + 4 * hi;
-                const f32x4 v = {o[dblk][4 * g] * inv, o[dblk][4 * g + 1] * inv,
-                                 o[dblk][4 * g + 2] * inv, o[dblk][4 * g + 3] * inv};
-                if (ot == KD_FA_TYPE_F32) {
-                    *reinterpret_cast<f32x4 *>(op + d * 4) = v;
-                } else if (ot == KD_FA_TYPE_BF16) {
-                    const u32x2 w = {Elem<__bf16>::pack2(v.x, v.y), Elem<__bf16>::pack2(v.z, v.w)};
-                    *reinterpret_cast<u32x2 *>(op + d * 2) = w;
-                } else {
-                    const u32x2 w = {Elem<_Float16>::pack2(v.x, v.y), Elem<_Float16>::pack2(v.z, v.w)};
-                    *reinterpret_cast<u32x2 *>(op + d * 2) = w;
-                }
+                const f32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) f32x4 *>(
+                    lds + wave * 32768 + ((qb * 4 + dblk) * 4 + g) * 1024 + lane * 16);
+                o[dblk][4 * g] = v.x;
+                o[dblk][4 * g + 1] = v.y;
+                o[dblk][4 * g + 2] = v.z;
+                o[dblk][4 * g + 3] = v.w;
             }
+        const float l_half = *reinterpret_cast<const __attribute__((address_space(3))) float *>(
+            lds + kW64LOff + wave * 512 + qb * 256 + lane * 4);
+        store_o_row(a, qt * 256 + wave * 64 + qb * 32 + l32, h, b, hi, o, l_half);
     }
+}
+
+template <typename T>
+static hipError_t launch_w64_t(const Args &a, hipStream_t s) {
+    switch (a.rope_mode) {
+    case KD_FA_ROPE_TABLE:
+        hipLaunchKernelGGL((fa_fwd_w64<T, KD_FA_ROPE_TABLE>), dim3(a.n_blocks), dim3(256), 0, s, a);
+        break;
+    case KD_FA_ROPE_AXES:
+        hipLaunchKernelGGL((fa_fwd_w64<T, KD_FA_ROPE_AXES>), dim3(a.n_blocks), dim3(256), 0, s, a);
+        break;
+    default:
+        hipLaunchKernelGGL((fa_fwd_w64<T, KD_FA_ROPE_NONE>), dim3(a.n_blocks), dim3(256), 0, s, a);
+        break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_w64(const Args &a, int kv_type, hipStream_t stream) {
+    return kv_type == KD_FA_TYPE_BF16 ? launch_w64_t<__bf16>(a, stream) : launch_w64_t<_Float16>(a, stream);
 }
 
 template <typename T, bool M, int R, bool KR>
