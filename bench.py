@@ -168,8 +168,9 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic_from_profile(),
-                     "kernel": "kdfa::fa_fwd_d128<bf16, mask=0, rope=Q, K from workspace>; "
-                               "the step also holds the K rotation pass (rope_k_kernel, <1% of it)",
+                     "kernel": "kdfa::fa_fwd_w64<bf16, RoPE table on Q, K from workspace> (64 query rows "
+                               "per wave); achieved is over the whole step, which also holds the K "
+                               "rotation pass (rope_k_kernel, <1% of it)",
                      "flop_per_launch": flop},
     }
 

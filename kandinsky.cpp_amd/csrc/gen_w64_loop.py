@@ -17,7 +17,8 @@ another tile of the same wave.  Per 64-key tile t (step t):
 Every arithmetic step is the one the 32-row kernel (kd_fa_kernel.hip)
 performs, in the same order per row -- the same MFMA accumulation order over
 k-steps and key steps, the same fma / exp2 / rounding, the same row sums
-(one dot2 chain per 16-key step, combined as (s0 + s1) + (s2 + s3)), the
+(the F32 weights of each 16-key step added in order, the steps combined as
+(s0 + s1) + (s2 + s3)), the
 same lazy-max rule decided per 32-row block -- so the two kernels give
 bitwise identical results.
 
@@ -47,8 +48,7 @@ LH = (230, 231)        # running half-row weight sum
 # 64) and two partial sums of 16-key steps
 PS = ((232, 233, 234), (235, 236, 237))
 X, Y = 238, 239
-ONE = 240              # the operand-type pair (1, 1)
-W_BASE = 241           # 7 slow-path temporaries (241..247)
+W_BASE = 240           # slow-path temporaries (240..247)
 V_LAST = 247
 # AGPRs
 A_O = 0                # O[qb][dblk] -> +64*qb + 16*dblk, 16 floats
@@ -68,6 +68,11 @@ S_FIRST, S_LAST = 84, 95
 KBUF = (0, 16384)
 VBUF = (32768, 49152)
 Q_OFF = 65536
+
+# Phase 1 schedule: VALU instructions after each MFMA, and the MFMA after
+# which the row check runs (the rest of S(t+1) is computed meanwhile)
+PER1 = int(os.environ.get("KD_W64_PER1", "4"))
+CHECK_AT = int(os.environ.get("KD_W64_CHECK_AT", "30"))
 
 MFMA_WS = 20           # MFMA result -> VALU / LDS / accvgpr access
 VALU_MFMA_WS = 4       # VALU or accvgpr write -> MFMA operand read
@@ -218,9 +223,6 @@ class Gen:
         self.T = T
         self.mfma = f"v_mfma_f32_32x32x16_{T}"
         self.cvt = {"bf16": "v_cvt_pk_bf16_f32", "f16": "v_cvt_pk_f16_f32"}[T]
-        self.dot, self.one = {"bf16": ("v_dot2c_f32_bf16", "0x3f803f80"),
-                              "f16": ("v_dot2c_f32_f16", "0x3c003c00")}[T]
-        self.dot3 = {"bf16": "v_dot2_f32_bf16", "f16": "v_dot2_f32_f16"}[T]
         self.slow = []      # out-of-line blocks (lists of lines)
 
     # ---------------------------------------------------------- streams
@@ -274,8 +276,9 @@ class Gen:
     def softmax_half(self, sp, pp, half, qbs, finish):
         """VALU stream: weights of keys 32*half .. +31 of S[sp] for the query
         blocks qbs (pairs of blocks interleaved), rounded into P[pp]; each
-        16-key step's row sum is a 4-long dot2 chain.  finish: half 0 leaves
-        s0 + s1 in PS[qb][0]; half 1 leaves (s0 + s1) + (s2 + s3) there."""
+        16-key step's row sum adds its 8 F32 weights in order (one add chain
+        per step).  finish: half 0 leaves s0 + s1 in PS[qb][0]; half 1 leaves
+        (s0 + s1) + (s2 + s3) there."""
         pairs = [(qb, k) for k in range(8) for qb in qbs]
         n = len(pairs)
         out = []
@@ -300,9 +303,10 @@ class Gen:
                 acc = PS[qb][1 + (kst & 1)]
                 out.append(valu(f"{self.cvt} {vr(w)}, {vr(e)}, {vr(e + 1)}", {vr(e), vr(e + 1)}, {vr(w)}))
                 if j == 0:
-                    out.append(Ins(f"{self.dot3} {vr(acc)}, {vr(w)}, {vr(ONE)}, 0", "dot", {vr(w), vr(ONE)}, {vr(acc)}))
+                    out.append(valu(f"v_add_f32 {vr(acc)}, {vr(e)}, {vr(e + 1)}", {vr(e), vr(e + 1)}, {vr(acc)}))
                 else:
-                    out.append(Ins(f"{self.dot} {vr(acc)}, {self.one}, {vr(w)}", "dot", {vr(w), vr(acc)}, {vr(acc)}))
+                    for h in range(2):
+                        out.append(valu(f"v_add_f32 {vr(acc)}, {vr(acc)}, {vr(e + h)}", {vr(acc), vr(e + h)}, {vr(acc)}))
         for qb in qbs:
             h01, a, b = PS[qb]
             if half == 0:
@@ -326,28 +330,42 @@ class Gen:
                 Ins(f"s_cselect_b32 s{base + 2}, 0, s{base + 2}", "salu")]
 
     # ------------------------------------------------------------ pieces
-    def merge(self, tr, seq, valus, extra=(), per=3):
+    def merge(self, tr, seq, valus, extra=(), per=3, tail=None, tail_at=None):
         """MFMAs in order, reads ahead of them, `per` VALU after each,
-        `extra` (SALU/VMEM groups) one group after each of the first MFMAs."""
+        `extra` (SALU/VMEM groups) one group after each of the first MFMAs;
+        `tail` (emitting code) after MFMA tail_at - 1 and all of `valus`."""
         vi = 0
         extra = list(extra)
+        tail_at = len(seq) if tail_at is None else tail_at
+
+        def finish():
+            nonlocal vi
+            for grp in extra:
+                for x in grp:
+                    tr.emit(x)
+            extra.clear()
+            while vi < len(valus):
+                tr.emit(valus[vi])
+                vi += 1
+            if tail:
+                tail(tr)
+
         for n, (before, m) in enumerate(seq):
+            if n == tail_at:
+                finish()
             for r in before:
                 tr.emit(r)
             tr.emit(m)
             if n >= 1 and extra:
                 for x in extra.pop(0):
                     tr.emit(x)
-            for _ in range(per):
-                if vi < len(valus):
-                    tr.emit(valus[vi])
-                    vi += 1
-        for grp in extra:
-            for x in grp:
-                tr.emit(x)
-        while vi < len(valus):
-            tr.emit(valus[vi])
-            vi += 1
+            if n < tail_at:
+                for _ in range(per):
+                    if vi < len(valus):
+                        tr.emit(valus[vi])
+                        vi += 1
+        if tail_at >= len(seq):
+            finish()
 
     def check(self, tr, p, tag):
         """Row-sum check of both query blocks: one v_permlane32_swap of the
@@ -430,20 +448,24 @@ class Gen:
         """Step t with parity p: S(t) in S[p], K(t+1) in KBUF[1-p], V(t) in
         VBUF[p]; P[p] holds the weights of keys 0-31 of tile t."""
         q = 1 - p
+        vpre, vseq = self.pv_stream(VBUF[p], p)
+
+        def tail(tr):
+            for r in vpre:
+                tr.emit(r)
+            self.check(tr, p, tag)
+
         if not final:
             pre, seq = self.qk_stream(KBUF[q], q)
             for r in pre:
                 tr.emit(r)
             dmas = [self.dma("v", VBUF[q], j) for j in range(4)] + [self.advance("v")] + \
                    [self.dma("k", KBUF[p], j) for j in range(4)] + [self.advance("k")]
-            self.merge(tr, seq, self.softmax_half(p, p, 1, (0, 1), True), dmas)
+            self.merge(tr, seq, self.softmax_half(p, p, 1, (0, 1), True), dmas, PER1, tail, CHECK_AT)
         else:
             for x in self.softmax_half(p, p, 1, (0, 1), True):
                 tr.emit(x)
-        vpre, vseq = self.pv_stream(VBUF[p], p)
-        for r in vpre:
-            tr.emit(r)
-        self.check(tr, p, tag)
+            tail(tr)
         if not final:
             self.merge(tr, vseq, self.softmax_half(q, q, 0, (0, 1), True))
             tr.raw("s_waitcnt vmcnt(0)")
@@ -455,7 +477,6 @@ class Gen:
     def build(self):
         tr = Tracker()
         e = tr.emit
-        e(valu(f"v_mov_b32 {vr(ONE)}, {self.one}", (), {vr(ONE)}))
         for qb in range(2):
             e(valu(f"v_mov_b32 {vr(M[qb])}, 0xff800000", (), {vr(M[qb])}))
             e(valu(f"v_mov_b32 {vr(LH[qb])}, 0", (), {vr(LH[qb])}))

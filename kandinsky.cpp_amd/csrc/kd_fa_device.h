@@ -58,11 +58,6 @@ template <> struct Elem<__bf16> {
     }
     static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
     static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-    // acc + lo(w) + hi(w), exact products by 1.0 (v_dot2c_f32_bf16)
-    static __device__ __forceinline__ float sum2(uint32_t w, float acc) {
-        const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one, acc, false);
-    }
 };
 
 template <> struct Elem<_Float16> {
@@ -76,10 +71,6 @@ template <> struct Elem<_Float16> {
     }
     static __device__ __forceinline__ float lo(uint32_t w) { return (float)__builtin_bit_cast(f16x2, w).x; }
     static __device__ __forceinline__ float hi(uint32_t w) { return (float)__builtin_bit_cast(f16x2, w).y; }
-    static __device__ __forceinline__ float sum2(uint32_t w, float acc) {
-        const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
-        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, acc, false);
-    }
 };
 
 static __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }

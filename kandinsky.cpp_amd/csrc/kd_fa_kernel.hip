@@ -439,20 +439,18 @@ void fa_fwd_d128(Args a) {
         }
     };
 
-    // P rounded to the operand type (the PV B operands); the row sum uses
-    // the same rounded weights as the numerator
-    // the sum of each 16-key step is its own dot2 chain (short dependency
-    // chains), the four combined as (s0 + s1) + (s2 + s3)
+    // P rounded to the operand type (the PV B operands).  The row sum adds the F32 weights (before rounding): each 16-key step's
+    // 8 weights of this lane in order, the four steps combined as
+    // (s0 + s1) + (s2 + s3).  (Plain adds: a dot2 on the rounded pairs would
+    // stall the matrix pipe.)
     auto pack_sum = [&](const float *p, vec8 pb[4]) -> float {
         float part[4];
 #pragma unroll
         for (int kst = 0; kst < 4; ++kst) {
             u32x4 w;
-            part[kst] = 0.0f;
-            for (int j = 0; j < 4; ++j) {
-                w[j] = E::pack2(p[8 * kst + 2 * j], p[8 * kst + 2 * j + 1]);
-                part[kst] = E::sum2(w[j], part[kst]);
-            }
+            for (int j = 0; j < 4; ++j) w[j] = E::pack2(p[8 * kst + 2 * j], p[8 * kst + 2 * j + 1]);
+            part[kst] = p[8 * kst] + p[8 * kst + 1];
+            for (int i = 2; i < 8; ++i) part[kst] += p[8 * kst + i];
             pb[kst] = __builtin_bit_cast(vec8, w);
         }
         return (part[0] + part[1]) + (part[2] + part[3]);
