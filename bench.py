@@ -216,6 +216,18 @@ def main():
         bytes2b = bytes2 - out2.numel() * 2
         sec["cross_attn_norm_bf16out_ms"] = round(ms2b, 4)
         sec["cross_attn_norm_bf16out_GBps"] = round(bytes2b / (ms2b * 1e-3) / 1e9, 1)
+        # the 2-D VAE's attention block (one head, D = 512, Q F32, K/V F16)
+        # at 64x64 and 128x128 latents (512- and 1024-pixel images)
+        for L5 in (4096, 16384):
+            q5 = rand(torch, (1, 1, L5, 512), 41, dev, torch.float32)
+            k5 = rand(torch, (1, 1, L5, 512), 42, dev, torch.float16)
+            v5 = rand(torch, (1, 1, L5, 512), 43, dev, torch.float16)
+            o5 = torch.empty((1, L5, 1, 512), device=dev, dtype=torch.float32)
+            d5 = kd_fa.make_desc(q5, k5, v5, None, o5, 512 ** -0.5)
+            ms5v = time_launches(torch, lambda: kd_fa.run_desc(d5, None, stream), 20, 3, stream)
+            sec[f"vae_attn_{L5}_ms"] = round(ms5v, 4)
+            sec[f"vae_attn_{L5}_tflops"] = round(4.0 * L5 * L5 * 512 / (ms5v * 1e-3) / 1e12, 2)
+            del q5, k5, v5, o5
         # 60 x (self + cross) with fresh buffers per layer (3 rotating sets)
         sets = [(q, k, v)] + [tuple(rand(torch, (B, HEADS, L, D), 10 * s + j, dev, bf) for j in range(3))
                               for s in range(1, 3)]

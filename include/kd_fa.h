@@ -28,6 +28,9 @@
  *   dst  [Dv, H, Lq, B]     F32 (ggml's permuted result); or BF16 / F16,
  *                           O rounded to nearest even on store -- the cast
  *                           the reference's out_layer input takes, fused
+ *   Dk = Dv = 128 (the DiT heads, src/models/crossdit.hpp:121-160) or 512
+ *   (the VAE's one-head attention block, src/models/vae.hpp:60-101: no
+ *   mask, no RoPE and no norm on that size); other sizes: KD_FA_ERR_SHAPE.
  *   dst[b][i][h][:] = sum_j softmax_j(scale * <q_bhi, k_j> + mask[b,h,i,j]) v_j
  *   with h_kv = h / (H / Hkv) and b_kv = b / (B / Bk).  A row whose keys
  *   are all masked (-inf) is written as zeros.

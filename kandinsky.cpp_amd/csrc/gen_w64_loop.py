@@ -53,9 +53,14 @@ V_LAST = 247
 # AGPRs
 A_O = 0                # O[qb][dblk] -> +64*qb + 16*dblk, 16 floats
 A_Q = 128              # Q[qb][ks] -> +32*qb + 4*ks
-A_KF = 192             # K fragments: 3 slots x 2 key blocks x 4
-A_VF = 216             # V^T fragments: 4 slots x 4
-A_LAST = 231
+# LDS operand prefetch distances: K fragments KPRE k-steps ahead, V^T
+# fragments VPRE fragments ahead (ring slots: KPRE + 1 and VPRE + 2)
+KPRE = int(os.environ.get("KD_W64_KPRE", "2"))
+VPRE = int(os.environ.get("KD_W64_VPRE", "2"))
+A_KF = 192             # K fragments: (KPRE + 1) slots x 2 key blocks x 4
+A_VF = A_KF + 8 * (KPRE + 1)   # V^T fragments: (VPRE + 2) slots x 4
+A_LAST = A_VF + 4 * (VPRE + 2) - 1
+assert A_LAST <= 255
 # SGPRs s84..s95
 S_K = 84               # s[84:87] K buffer resource (moves one tile per DMA)
 S_V = 88               # s[88:91] V buffer resource
@@ -230,13 +235,13 @@ class Gen:
         """S[sp] = K(kbuf) Q^T: (pre-reads, [(reads before, mfma)])."""
         reads = {}
         for ks in range(8):
-            slot = ks % 3
+            slot = ks % (KPRE + 1)
             reads[ks] = [Ins(f"ds_read_b128 {arng(A_KF + 8 * slot + 4 * kb, 4)}, %[krd{ks}] offset:{kbuf + kb * 8192}",
                              "lds_rd", (), aset(A_KF + 8 * slot + 4 * kb, 4)) for kb in range(2)]
-        pre = reads[0] + reads[1]
+        pre = sum((reads[ks] for ks in range(KPRE)), [])
         seq = []
         for ks in range(8):
-            slot = ks % 3
+            slot = ks % (KPRE + 1)
             n = 0
             for kb in range(2):
                 for qb in range(2):
@@ -245,7 +250,7 @@ class Gen:
                     b = A_Q + 32 * qb + 4 * ks
                     c = "0" if ks == 0 else vrng(d, 16)
                     rd = aset(a, 4) | aset(b, 4) | (set() if ks == 0 else vset(d, 16))
-                    before = reads[ks + 2] if (n == 1 and ks + 2 < 8) else []
+                    before = reads[ks + KPRE] if (n == 1 and ks + KPRE < 8) else []
                     seq.append((before, Ins(f"{self.mfma} {vrng(d, 16)}, {arng(a, 4)}, {arng(b, 4)}, {c}",
                                             "mfma", rd, vset(d, 16))))
                     n += 1
@@ -255,20 +260,20 @@ class Gen:
         """O += V(vbuf)^T P[pp]^T: (pre-reads, [(reads before, mfma)])."""
         def frag_reads(f):
             kst, dblk = divmod(f, 4)
-            s = A_VF + 4 * (f % 4)
+            s = A_VF + 4 * (f % (VPRE + 2))
             off = vbuf + 4096 * kst
             return [Ins(f"ds_read_b64_tr_b16 {arng(s, 2)}, %[vrd{dblk}] offset:{off}", "lds_rd", (), aset(s, 2)),
                     Ins(f"ds_read_b64_tr_b16 {arng(s + 2, 2)}, %[vrd{dblk}] offset:{off + 1024}", "lds_rd", (),
                         aset(s + 2, 2))]
-        pre = frag_reads(0) + frag_reads(1)
+        pre = sum((frag_reads(f) for f in range(VPRE)), [])
         seq = []
         for f in range(16):
             kst, dblk = divmod(f, 4)
-            s = A_VF + 4 * (f % 4)
+            s = A_VF + 4 * (f % (VPRE + 2))
             for qb in range(2):
                 o = A_O + 64 * qb + 16 * dblk
                 p = P_BASE[pp] + 16 * qb + 4 * kst
-                before = frag_reads(f + 2) if (qb == 1 and f + 2 < 16) else []
+                before = frag_reads(f + VPRE) if (qb == 1 and f + VPRE < 16) else []
                 seq.append((before, Ins(f"{self.mfma} {arng(o, 16)}, {arng(s, 4)}, {vrng(p, 4)}, {arng(o, 16)}",
                                         "mfma", aset(o, 16) | aset(s, 4) | vset(p, 4), aset(o, 16))))
         return pre, seq

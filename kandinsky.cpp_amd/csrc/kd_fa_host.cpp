@@ -16,6 +16,8 @@
 namespace {
 
 constexpr int64_t kHeadDim = 128;
+// D of the 2-D VAE's single-head attention (src/models/vae.hpp:60-101)
+constexpr int64_t kHeadDimVae = 512;
 constexpr int64_t kI32Max = 0x7fffffff;
 // A 64-row tile is addressed with 32-bit offsets from a per-tile base.
 constexpr uint64_t kMaxRowStride = (uint64_t)1 << 25;
@@ -50,7 +52,8 @@ int validate(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, b
     // shapes
     for (int i = 0; i < 4; ++i)
         if (q.ne[i] < 0 || k.ne[i] < 0 || v.ne[i] < 0 || o.ne[i] < 0) return KD_FA_ERR_SHAPE;
-    if (q.ne[0] != kHeadDim || k.ne[0] != kHeadDim || v.ne[0] != kHeadDim) return KD_FA_ERR_SHAPE;
+    const int64_t D = q.ne[0];
+    if (k.ne[0] != D || v.ne[0] != D || (D != kHeadDim && D != kHeadDimVae)) return KD_FA_ERR_SHAPE;
     const int64_t Lq = q.ne[1], Lk = k.ne[1], H = q.ne[2], B = q.ne[3];
     if (v.ne[1] != Lk) return KD_FA_ERR_SHAPE;
     if (k.ne[2] == 0 || v.ne[2] == 0 || k.ne[3] == 0 || v.ne[3] == 0) return KD_FA_ERR_SHAPE;
@@ -78,6 +81,16 @@ int validate(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, b
         mv = is_16b(m.data) && is_16b(m.nb[1]) && is_16b(m.nb[2]) && is_16b(m.nb[3]);
     }
     if (mask_vec) *mask_vec = mv;
+
+    // D = 512 (the VAE attention block): the plain node only -- no mask, no
+    // RoPE, no RMSNorm; 32-row query tiles; 32-bit V row offsets
+    if (D == kHeadDimVae) {
+        if (m.data) return KD_FA_ERR_SHAPE;
+        if ((r && r->mode != KD_FA_ROPE_NONE) || (n && (n->q_weight || n->k_weight))) return KD_FA_ERR_ROPE;
+        if (H > 0 && B > 0 && (Lq + 31) / 32 > kI32Max / H / B) return KD_FA_ERR_SHAPE;
+        if (Lk > 0 && (Lk - 1) * v.nb[1] + 1024 >= (int64_t)1 << 32) return KD_FA_ERR_LAYOUT;
+        return KD_FA_OK;
+    }
 
     // RoPE
     if (r && r->mode != KD_FA_ROPE_NONE) {
@@ -209,6 +222,11 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
         a.rcp_w = 1.0f / (float)r->grid[2];
     }
     hipStream_t hs = static_cast<hipStream_t>(stream);
+    if (d->q.ne[0] == kHeadDimVae) {
+        a.n_qt = (int32_t)((Lq + 31) / 32);
+        a.n_blocks = (int32_t)(a.n_qt * H * B);
+        return kdfa::launch_d512(a, d->v.type, hs) == hipSuccess ? KD_FA_OK : KD_FA_ERR_LAUNCH;
+    }
     bool k_rope = k_xform && !ws;
     const int rows = kdfa::block_rows(a.m != nullptr, k_rope);
     a.n_qt = (int32_t)((Lq + rows - 1) / rows);

@@ -55,6 +55,9 @@ hipError_t launch(const Args &a, int kv_type, bool k_rope, hipStream_t stream);
 // multiple of 64; query tiles of 256 rows like the unmasked launch).
 hipError_t launch_w64(const Args &a, int kv_type, hipStream_t stream);
 
+// Enqueue the D = 512 kernel (no mask, no RoPE; 32-row query tiles).
+hipError_t launch_d512(const Args &a, int kv_type, hipStream_t stream);
+
 // Normalise (kn_w) and rotate (RoPE mode) K ([D, Lk, H/rk2, B/rk3] through
 // a.k and its strides) into `out`, contiguous, in K's type.
 hipError_t launch_rope_k(const Args &a, int kv_type, int k_heads, int k_batch, void *out, hipStream_t stream);

@@ -262,14 +262,18 @@ def out_shape(q, v):
 # operator entry points
 # ---------------------------------------------------------------------------
 
-def supports(q, k, v, mask=None, dst=None, scale=1.0, max_bias=0.0, logit_softcap=0.0, rope=None):
-    """(ok, reason): the kd_fa_supports / kd_fa_rope_supports answer."""
+def supports(q, k, v, mask=None, dst=None, scale=1.0, max_bias=0.0, logit_softcap=0.0, rope=None, norm=None):
+    """(ok, reason): the kd_fa_supports / kd_fa_rope_supports /
+    kd_fa_dit_supports (with ``norm``) answer."""
     torch = _torch()
     if dst is None:
         dst = torch.empty(out_shape(q, v), dtype=torch.float32, device=q.device)
     d = make_desc(q, k, v, mask, dst, scale, max_bias, logit_softcap)
     reason = ctypes.c_int(0)
-    if rope is None:
+    if norm is not None:
+        ok = _lib().kd_fa_dit_supports(ctypes.byref(d), ctypes.byref(rope) if rope is not None else None,
+                                       ctypes.byref(norm), ctypes.byref(reason))
+    elif rope is None:
         ok = _lib().kd_fa_supports(ctypes.byref(d), ctypes.byref(reason))
     else:
         ok = _lib().kd_fa_rope_supports(ctypes.byref(d), ctypes.byref(rope), ctypes.byref(reason))

@@ -105,6 +105,29 @@ def test_accepts_reference_node(qt, kt):
     assert _sup(*_node(qt=qt, kt=kt, H=8, Hkv=2)) == (True, 0)
 
 
+def test_vae_node_d512():
+    """The 2-D VAE attention block's node (vae.hpp:60-101: one head, D = 512,
+    Q F32, K/V F16) is accepted plain; a mask, RoPE or RMSNorm weights with
+    D = 512 are not, nor any D other than 128 and 512."""
+    def node(D, Lq=64, Lk=48, B=1, H=1):
+        q = torch.zeros((B, H, Lq, D), dtype=torch.float32)
+        k = torch.zeros((B, H, Lk, D), dtype=torch.float16)
+        v = torch.zeros((B, H, Lk, D), dtype=torch.float16)
+        dst = torch.zeros((B, Lq, H, D), dtype=torch.float32)
+        return q, k, v, dst
+    q, k, v, dst = node(512)
+    assert _sup(q, k, v, None, dst, scale=512 ** -0.5) == (True, 0)
+    assert _sup(*[t.to(torch.bfloat16) if t is not q and t is not dst else t for t in (q, k, v)], None, dst) == (True, 0)
+    assert _sup(q, k, v, None, dst.half()) == (True, 0)
+    assert _sup(q, k, v, torch.zeros((1, 1, 64, 48), dtype=torch.float16), dst) == (False, kd_fa.ERR_SHAPE)
+    buf = torch.zeros(4096, dtype=torch.float32)
+    assert _sup(q, k, v, None, dst, rope=kd_fa.rope_axes(buf, (3, 4, 5), (32, 48, 48))) == (False, kd_fa.ERR_ROPE)
+    w = torch.ones(512, dtype=torch.float32)
+    assert _sup(q, k, v, None, dst, norm=kd_fa.qk_norm(w, None)) == (False, kd_fa.ERR_ROPE)
+    for D in (64, 256, 384, 1024):
+        assert _sup(*node(D)[:3], None, node(D)[3]) == (False, kd_fa.ERR_SHAPE)
+
+
 def test_rejections_carry_reason():
     q, k, v, m, dst = _node()
     assert _sup(q[..., :64], k[..., :64], v[..., :64], None, dst[..., :64]) == (False, kd_fa.ERR_SHAPE)
