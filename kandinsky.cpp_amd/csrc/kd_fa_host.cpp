@@ -4,6 +4,7 @@
 // keeps pointers past the call.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <cstdlib>
@@ -164,6 +165,34 @@ static bool use_w64(const kdfa::Args &a, bool k_on_load) {
     return (int64_t)(a.Lk - 1) * a.k_nb1 + 256 < lim && (int64_t)(a.Lk - 1) * a.v_nb1 + 256 < lim;
 }
 
+// Short key sets (the text cross-attention) go to the kernel that keeps K
+// and V in LDS, when K is read as stored, Q is not rotated and stored as F32
+// or in K's type, and a mask's rows are 16-byte aligned and hold every
+// 8-key chunk that starts below Lk.  KD_FA_XRES=0 in the environment routes
+// them to the 32-row kernel (for comparisons).
+static bool use_xres(const kdfa::Args &a, const kd_fa_desc *d, bool k_on_load) {
+    const char *e = std::getenv("KD_FA_XRES");
+    if ((e && e[0] == '0') || k_on_load || a.rope_mode != KD_FA_ROPE_NONE) return false;
+    if (a.Lk > kdfa::kXresMaxKeys) return false;
+    if (a.q_type != KD_FA_TYPE_F32 && a.q_type != d->v.type) return false;
+    if (a.m && (!a.mask_vec || d->mask.ne[0] < ((int64_t)a.Lk + 7) / 8 * 8)) return false;
+    return true;
+}
+
+// Query ranges per (b, h) for fa_fwd_xres: about one workgroup per CU
+// (256 on MI355X) in all, at least four 32-row blocks (one per wave) each.
+static void xres_split(kdfa::Args &a) {
+    const int64_t n_qb = ((int64_t)a.Lq + 31) / 32;
+    const int64_t bh = (int64_t)a.H * a.B;
+    int64_t ranges = (256 + bh - 1) / bh;
+    ranges = std::min<int64_t>(ranges, (n_qb + 3) / 4);
+    ranges = std::max<int64_t>(ranges, 1);
+    const int64_t per = (n_qb + ranges - 1) / ranges;
+    a.x_blocks = (int32_t)per;
+    a.n_qt = (int32_t)((n_qb + per - 1) / per);
+    a.n_blocks = (int32_t)(a.n_qt * bh);
+}
+
 int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *ws, size_t ws_bytes,
         void *stream) {
     bool mask_vec = false;
@@ -245,8 +274,13 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
         a.k_nb2 = row * a.Lk;
         a.k_nb3 = row * a.Lk * hk;
     }
-    const hipError_t e = use_w64(a, k_rope) ? kdfa::launch_w64(a, d->v.type, hs)
-                                            : kdfa::launch(a, d->v.type, k_rope, hs);
+    hipError_t e;
+    if (use_xres(a, d, k_rope)) {
+        xres_split(a);
+        e = kdfa::launch_xres(a, d->v.type, hs);
+    } else {
+        e = use_w64(a, k_rope) ? kdfa::launch_w64(a, d->v.type, hs) : kdfa::launch(a, d->v.type, k_rope, hs);
+    }
     if (e != hipSuccess) return KD_FA_ERR_LAUNCH;
     return KD_FA_OK;
 }

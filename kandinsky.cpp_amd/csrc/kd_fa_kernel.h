@@ -37,8 +37,9 @@ struct Args {
     int32_t grid_t, grid_h, grid_w;
     int32_t axis0, axis1, axis2;
     float rcp_h, rcp_w;   // 1.0f / grid_h, 1.0f / grid_w
-    int32_t n_qt;       // query tiles per (b, h)
+    int32_t n_qt;       // query tiles per (b, h) (fa_fwd_xres: query ranges)
     int32_t n_blocks;   // n_qt * H * B
+    int32_t x_blocks;   // fa_fwd_xres: 32-row query blocks per range
     int32_t heads_inner;  // block order: heads fastest (mask shared by all heads)
     int32_t o_type;       // dst element type: F32, F16 or BF16
     const float *qn_w;    // RMSNorm weight of Q (F32 [128]) or nullptr
@@ -54,6 +55,12 @@ hipError_t launch(const Args &a, int kv_type, bool k_rope, hipStream_t stream);
 // Enqueue the 64-rows-per-wave kernel (no mask, K as stored, Lk a positive
 // multiple of 64; query tiles of 256 rows like the unmasked launch).
 hipError_t launch_w64(const Args &a, int kv_type, hipStream_t stream);
+
+// Enqueue the short-key kernel (K as stored, no RoPE, Lk <= kXresMaxKeys):
+// K and V of a (batch, head) held in LDS, n_qt ranges of x_blocks 32-row
+// query blocks per (b, h).
+constexpr int kXresMaxKeys = 256;
+hipError_t launch_xres(const Args &a, int kv_type, hipStream_t stream);
 
 // Enqueue the D = 512 kernel (no mask, no RoPE; 32-row query tiles).
 hipError_t launch_d512(const Args &a, int kv_type, hipStream_t stream);

@@ -754,6 +754,461 @@ void fa_fwd_d128(Args a) {
 }
 
 // ---------------------------------------------------------------------------
+// fa_fwd_xres: short key sets held in LDS -- the text cross-attention
+// (src/models/crossdit.hpp:174-200: a few hundred prompt tokens as keys
+// against every visual token as a query).  With Lk <= 256, K and V of one
+// (batch, head) are at most 2 x 64 KiB, and the call's cost is streaming Q
+// rows in and O rows out (plus the mask rows, which all heads share).
+//
+// One workgroup = 8 waves, two per SIMD = one (batch, head) and a range of
+// 32-row query blocks (a.x_blocks of them); wave w takes blocks w, w+8, ...
+// K and V are loaded into LDS once, in fa_fwd_d128's tile layout; after that
+// the waves never synchronise again, and while one wave of a SIMD waits for
+// its next block's Q and mask rows, the other computes.  Within a block the
+// mask chunks of tile t+1 are loaded while tile t's products are computed.  Workgroups
+// are dealt heads-fastest and XCD-contiguous: the heads of one query range
+// run on one XCD and share its L2 for the mask rows.
+//
+// Per row the arithmetic is fa_fwd_d128's -- the same products, the same
+// online softmax (masked: exact running max; unmasked: the lazy max with the
+// weight-sum check), the same sums and the same store -- so the two kernels
+// give bitwise equal results.
+constexpr int kXNT = 4;      // key tiles held in LDS: Lk <= 256
+constexpr int kXWaves = 8;
+constexpr int kXStage = 2048;   // per wave: 16 rows x 128 bytes of O
+static_assert(kXNT * kBN == kXresMaxKeys, "LDS holds every key");
+
+template <typename T, bool HAS_MASK, bool Q32>
+__global__ __launch_bounds__(64 * kXWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void fa_fwd_xres(Args a) {
+    constexpr int kThreads = 64 * kXWaves;
+    constexpr int kRounds = kTileBytes / (kThreads * 16);
+    static_assert(kRounds * kThreads * 16 == kTileBytes, "tile shape");
+    typedef Elem<T> E;
+    typedef typename E::vec8 vec8;
+    // one LDS object: K tiles at 0, V tiles at 64 KiB, a 2 KiB staging area
+    // per wave for its O rows, the query-norm weights -- so that every K
+    // fragment address is one base register plus an immediate offset (and
+    // every V address one more base)
+    __shared__ __attribute__((aligned(1024))) char lds[2 * kXNT * kTileBytes + kXWaves * kXStage + kD * 4];
+    lds_t *const sK = LDS_PTR(char, lds);
+    lds_t *const sV = sK + kXNT * kTileBytes;
+    float *const lQw = reinterpret_cast<float *>(lds + 2 * kXNT * kTileBytes + kXWaves * kXStage);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31;
+    const int hi = lane >> 5;
+
+    // unit (b, range, h), heads fastest; each XCD a contiguous run of units
+    const int pid = blockIdx.x;
+    const int per = a.n_blocks >> 3;
+    const int lid = pid < per * 8 ? (pid & 7) * per + (pid >> 3) : pid;
+    const int h = lid % a.H;
+    const int rest = lid / a.H;
+    const int range = rest % a.n_qt;
+    const int b = rest / a.n_qt;
+
+    const char *kbase = a.k + (int64_t)(h / a.rk2) * a.k_nb2 + (int64_t)(b / a.rk3) * a.k_nb3;
+    const char *vbase = a.v + (int64_t)(h / a.rv2) * a.v_nb2 + (int64_t)(b / a.rv3) * a.v_nb3;
+    const int Lk = a.Lk;
+    const int n_tiles = (Lk + kBN - 1) / kBN;
+
+    // ---- K, V -> LDS (rows past Lk repeat key Lk - 1, as in fa_fwd_d128) ----
+    {
+        const int dma_row = lane >> 4;
+        const int dma_pc = lane & 15;
+#pragma unroll
+        for (int t = 0; t < kXNT; ++t) {
+            if (t < n_tiles) {
+                const char *kt = kbase + (int64_t)t * kBN * a.k_nb1;
+                const char *vt = vbase + (int64_t)t * kBN * a.v_nb1;
+#pragma unroll
+                for (int j = 0; j < kRounds; ++j) {
+                    const int r = 4 * (wave + kXWaves * j) + dma_row;
+                    const int kr = t * kBN + k_row_of(r) < Lk ? k_row_of(r) : Lk - 1 - t * kBN;
+                    const int vr = t * kBN + r < Lk ? r : Lk - 1 - t * kBN;
+                    dma16(kt, (uint32_t)kr * (uint32_t)a.k_nb1 + ((dma_pc ^ (r & 15)) << 4),
+                          sK + t * kTileBytes + (wave + kXWaves * j) * 1024);
+                    dma16(vt, (uint32_t)vr * (uint32_t)a.v_nb1 + ((dma_pc ^ v_swz(r)) << 4),
+                          sV + t * kTileBytes + (wave + kXWaves * j) * 1024);
+                }
+            }
+        }
+        if (a.qn_w && tid < kD / 4)
+            reinterpret_cast<f32x4 *>(lQw)[tid] = reinterpret_cast<const f32x4 *>(a.qn_w)[tid];
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+
+    const int n_qb = (a.Lq + 31) >> 5;
+    const int qb_end = min((range + 1) * a.x_blocks, n_qb);
+    int qb = range * a.x_blocks + wave;
+    if (qb >= qb_end) return;   // no barrier follows
+
+    const float c2 = __builtin_fabsf(a.scale_log2);
+    uint32_t k_rd[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) k_rd[ks] = l32 * 256 + (((2 * ks + hi) ^ (lane & 15)) << 4);
+    const int v_sub = (lane & 15) >> 2;
+    const int v_c_lo = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+    uint32_t v_rd[4];
+#pragma unroll
+    for (int dblk = 0; dblk < 4; ++dblk)
+        v_rd[dblk] = 2048 * hi + 256 * v_sub + (((4 * dblk + v_c_lo) ^ v_swz(v_sub)) << 4) + 8 * (lane & 1);
+
+    // ---- operands of a block ----------------------------------------------
+    // Q: this lane's 64 elements of its row as stored (Q32: F32, 16 x 16
+    // bytes; else K's type, 8 x 16 bytes).  Mask: this lane's 32 keys of a
+    // tile as four 16-byte chunks.  The mask rows hold every chunk that
+    // starts below Lk; chunks past it re-read the last one and, like the
+    // keys of a partial chunk past Lk, count as -inf.
+    const char *const qbase = a.q + (int64_t)h * a.q_nb2 + (int64_t)b * a.q_nb3;
+    const int64_t q_nb1 = a.q_nb1;
+    const char *const mbase = HAS_MASK ? a.m + (int64_t)(h % a.m_ne2) * a.m_nb2 + (int64_t)(b % a.m_ne3) * a.m_nb3
+                                       : nullptr;
+    const int64_t m_nb1 = a.m_nb1;
+    const int Lq = a.Lq;
+    const int o_type = a.o_type;
+    char *const obase = a.o + (int64_t)b * a.o_nb3 + (int64_t)h * a.o_nb1;
+    const int64_t o_nb2 = a.o_nb2;
+    lds_t *const sO = sV + kXNT * kTileBytes + wave * kXStage;
+    const bool qnorm = a.qn_w != nullptr;
+    const float norm_eps = a.norm_eps;
+    const bool qneg = a.scale_log2 < 0.0f;
+    u32x4 qraw[Q32 ? 16 : 8];
+    u32x4 mraw[4];
+    // hi_b, lk_b: hi and Lk, made opaque once per block so that the
+    // per-lane address offsets and per-key tests below are computed inside
+    // the block loop (hoisted out of it, they would hold dozens of registers
+    // for the whole loop)
+    int hi_b = hi, lk_b = Lk;
+    auto issue_q = [&](int q_ld) __attribute__((always_inline)) {
+        const char *qp = qbase + (int64_t)q_ld * q_nb1 + (Q32 ? 32 : 16) * hi_b;
+        if constexpr (Q32) {
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+                qraw[2 * ks] = ld16(qp + ks * 64);
+                qraw[2 * ks + 1] = ld16(qp + ks * 64 + 16);
+            }
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) qraw[ks] = ld16(qp + ks * 32);
+        }
+    };
+    auto issue_m = [&](const uint16_t *mrow, int t, u32x4 dst[4]) __attribute__((always_inline)) {
+        const int last_chunk = (lk_b - 1) & ~7;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int k0 = t * kBN + (c >> 1) * 32 + (c & 1) * 16 + hi_b * 8;
+            dst[c] = ld16(mrow + (k0 < last_chunk ? k0 : last_chunk));
+        }
+    };
+    // elements ks*16 + hi*8 .. +7 of the row as F32 (load8_f32 on the raw bytes)
+    auto q_elems = [&](int ks, float x[8]) __attribute__((always_inline)) {
+        if constexpr (Q32) {
+            const f32x4 u = __builtin_bit_cast(f32x4, qraw[2 * ks]);
+            const f32x4 w = __builtin_bit_cast(f32x4, qraw[2 * ks + 1]);
+            x[0] = u.x; x[1] = u.y; x[2] = u.z; x[3] = u.w;
+            x[4] = w.x; x[5] = w.y; x[6] = w.z; x[7] = w.w;
+        } else {
+            for (int j = 0; j < 4; ++j) { x[2 * j] = E::lo(qraw[ks][j]); x[2 * j + 1] = E::hi(qraw[ks][j]); }
+        }
+    };
+    // load_q_frags' arithmetic (RMSNorm, rounding, sign) on the raw bytes
+    vec8 qf[8];
+    auto q_frags = [&]() __attribute__((always_inline)) {
+        float qscale = 1.0f;
+        if (qnorm) {
+            double ss = 0.0;
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+                float x[8];
+                q_elems(ks, x);
+                ss += sum_sq8(x);
+            }
+            qscale = rms_scale(pair_sum_f64(ss), norm_eps);
+        }
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            const int d0 = ks * 16 + hi * 8;
+            float x[8];
+            q_elems(ks, x);
+            if (qnorm)
+                rms_apply8(x, qscale, *reinterpret_cast<const f32x4 *>(lQw + d0),
+                           *reinterpret_cast<const f32x4 *>(lQw + d0 + 4));
+            u32x4 w;
+            for (int j = 0; j < 4; ++j) w[j] = E::pack2(x[2 * j], x[2 * j + 1]);
+            if (qneg) w ^= (u32x4){0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
+            qf[ks] = __builtin_bit_cast(vec8, w);
+        }
+    };
+
+    f32x16 o[4];
+    float m_run, l_half;
+
+    auto qk = [&](const lds_t *ks_, f32x16 &s0, f32x16 &s1) __attribute__((always_inline)) {
+        constexpr int kKPre = HAS_MASK ? 1 : KD_FA_KPRE;
+        s0 = (f32x16){};
+        s1 = (f32x16){};
+        vec8 ka[8][2];
+#pragma unroll
+        for (int ks = 0; ks < kKPre; ++ks) {
+            ka[ks][0] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks]);
+            ka[ks][1] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks] + 32 * 256);
+        }
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            if (ks + kKPre < 8) {
+                ka[ks + kKPre][0] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks + kKPre]);
+                ka[ks + kKPre][1] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks + kKPre] + 32 * 256);
+            }
+            s0 = E::mfma(ka[ks][0], qf[ks], s0);
+            s1 = E::mfma(ka[ks][1], qf[ks], s1);
+        }
+        if constexpr (KD_FA_SCHED) sched_qk<kKPre>();
+    };
+    auto update_max = [&](float mx) __attribute__((always_inline)) {
+        if (__builtin_amdgcn_ballot_w64(mx > m_run + kTau) != 0) {
+            const float m_new = __builtin_fmaxf(m_run, mx);
+            const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            l_half *= alpha;
+#pragma unroll
+            for (int dblk = 0; dblk < 4; ++dblk)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[dblk][i] *= alpha;
+        }
+    };
+    auto pack_sum = [&](const float *p, vec8 pb[4]) -> float {
+        float part[4];
+#pragma unroll
+        for (int kst = 0; kst < 4; ++kst) {
+            u32x4 w;
+            for (int j = 0; j < 4; ++j) w[j] = E::pack2(p[8 * kst + 2 * j], p[8 * kst + 2 * j + 1]);
+            part[kst] = p[8 * kst] + p[8 * kst + 1];
+            for (int i = 2; i < 8; ++i) part[kst] += p[8 * kst + i];
+            pb[kst] = __builtin_bit_cast(vec8, w);
+        }
+        return (part[0] + part[1]) + (part[2] + part[3]);
+    };
+    auto pv = [&](const lds_t *vs_, const vec8 pb[4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int kst = 0; kst < 4; ++kst) {
+#pragma unroll
+            for (int dblk = 0; dblk < 4; ++dblk) {
+                const lds_t *vp = vs_ + v_rd[dblk] + 4096 * kst;
+                const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(vp));
+                const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(vp + 1024));
+                const vec8 va = __builtin_bit_cast(vec8, __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+                o[dblk] = E::mfma(va, pb[kst], o[dblk]);
+            }
+        }
+    };
+    // masked tile t with its mask chunks mr: logits s*c2 + mask*log2(e),
+    // -inf entries (and keys past Lk) stay -inf; a tile that is -inf for all
+    // 32 rows is skipped.  Element i of this lane is key
+    // t*64 + 32*(i/16) + 16*((i/8)%2) + 8*hi + i%8, chunk i/8.
+    auto tile_masked = [&](auto part_c, int t, u32x4 mr[4], const uint16_t *mrow) __attribute__((always_inline)) {
+        constexpr bool part = decltype(part_c)::value;
+        auto mval = [&](int i) __attribute__((always_inline)) -> float {
+            const uint32_t w = mr[i >> 3][(i & 7) >> 1];
+            const float v = (i & 1) ? f16_hi(w) : f16_lo(w);
+            if constexpr (part) {
+                const int key = t * kBN + (i >> 4) * 32 + ((i >> 3) & 1) * 16 + hi_b * 8 + (i & 7);
+                return key < lk_b ? v : -INFINITY;
+            }
+            return v;
+        };
+        bool any = false;
+        if constexpr (part) {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) any |= mval(i) != -INFINITY;
+        } else {
+            // on the F16 bits: -inf is exactly 0xfc00
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    any |= (mr[c][e] & 0xffffu) != 0xfc00u || (mr[c][e] >> 16) != 0xfc00u;
+        }
+        if (__builtin_amdgcn_ballot_w64(any) == 0) {
+            if (t + 1 < n_tiles) issue_m(mrow, t + 1, mr);
+            return;
+        }
+        f32x16 s0, s1;
+        qk(sK + t * kTileBytes, s0, s1);
+        float p[32];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            p[i] = s0[i];
+            p[16 + i] = s1[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            const float mv = mval(i);
+            p[i] = mv == -INFINITY ? -INFINITY : __builtin_fmaf(mv, kLog2e, p[i] * c2);
+        }
+        // the mask chunks are consumed: the registers take the next tile's
+        if (t + 1 < n_tiles) issue_m(mrow, t + 1, mr);
+        update_max(pair_max(max32(p)));
+        const float mu = m_run == -INFINITY ? 0.0f : m_run;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) p[i] = __builtin_amdgcn_exp2f(p[i] - mu);
+        vec8 pb[4];
+        l_half += pack_sum(p, pb);
+        pv(sV + t * kTileBytes, pb);
+    };
+    // unmasked tile: weights against the current running max, the exact max
+    // and a redo only when a row's weight sum leaves [0, kSumCap]; keys past
+    // Lk (repeats of key Lk - 1) get weight 0
+    auto tile_plain = [&](auto part_c, int t) __attribute__((always_inline)) {
+        constexpr bool tail = decltype(part_c)::value;
+        f32x16 s0, s1;
+        qk(sK + t * kTileBytes, s0, s1);
+        const int key0 = t * kBN;
+        auto drop_tail = [&](float *p) __attribute__((always_inline)) {
+            if constexpr (tail) {
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    const int key = key0 + (i >> 4) * 32 + 16 * ((i >> 3) & 1) + 8 * hi_b + (i & 7);
+                    p[i] = key < lk_b ? p[i] : 0.0f;
+                }
+            }
+        };
+        vec8 pb[4];
+        float p[32];
+        float nm = -m_run;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], c2, nm));
+            p[16 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], c2, nm));
+        }
+        drop_tail(p);
+        float sum = pack_sum(p, pb);
+        const float pair = pair_sum(sum);
+        if (__builtin_amdgcn_ballot_w64(!(pair <= kSumCap)) != 0) {
+            float q[32];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) { q[i] = s0[i]; q[16 + i] = s1[i]; }
+            update_max(pair_max(max32(q)) * c2);
+            nm = -m_run;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], c2, nm));
+                p[16 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], c2, nm));
+            }
+            drop_tail(p);
+            sum = pack_sum(p, pb);
+        }
+        l_half += sum;
+        pv(sV + t * kTileBytes, pb);
+    };
+
+    for (; qb < qb_end; qb += kXWaves) {
+        lk_b = Lk;
+        hi_b = hi;
+        asm volatile("" : "+s"(lk_b), "+v"(hi_b));
+        const int q_row = qb * 32 + l32;
+        const int q_ld = q_row < Lq ? q_row : Lq - 1;
+        issue_q(q_ld);
+        const uint16_t *mrow = nullptr;
+        if (HAS_MASK) {
+            mrow = reinterpret_cast<const uint16_t *>(mbase + (int64_t)q_ld * m_nb1);
+            issue_m(mrow, 0, mraw);
+        }
+        q_frags();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = (f32x16){};
+        m_run = -INFINITY;
+        l_half = 0.0f;
+#pragma unroll
+        for (int t = 0; t < kXNT; ++t) {
+            if (t < n_tiles) {
+                const bool part = (t + 1) * kBN > lk_b;   // the last tile, keys past Lk
+                if (HAS_MASK) {
+                    if (part)
+                        tile_masked(BC<true>(), t, mraw, mrow);
+                    else
+                        tile_masked(BC<false>(), t, mraw, mrow);
+                } else {
+                    if (part)
+                        tile_plain(BC<true>(), t);
+                    else
+                        tile_plain(BC<false>(), t);
+                }
+            }
+        }
+        // O / l -> the rows (store_o_row_l's arithmetic), through the wave's
+        // staging area, 16 rows at a time: the lanes of those rows leave
+        // their 16-byte pieces there (chunk index XOR the row's low bits: no
+        // bank conflicts), then lane L reads chunk L%8 of row 8j + L/8, so
+        // that every store instruction writes eight whole 128-byte lines (one
+        // per row) instead of 32-byte pieces of 32 rows.  F32: one 32-column
+        // block per round; 16-bit: two.  (LDS operations of a wave complete
+        // in order, so a round's reads see its writes and precede the next
+        // round's writes.)
+        {
+            const float l_run = pair_sum(l_half);
+            const float inv = l_run == 0.0f ? 0.0f : 1.0f / l_run;
+            const int rr = lane >> 3;
+            const int rc = lane & 7;
+            const int r16 = l32 & 15;
+            auto flush = [&](int half, int col_byte) __attribute__((always_inline)) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int r = 8 * j + rr;
+                    const u32x4 w = *reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(
+                        sO + r * 128 + ((rc ^ (r & 7)) << 4));
+                    const int row = qb * 32 + 16 * half + r;
+                    if (row < Lq) *reinterpret_cast<u32x4 *>(obase + (int64_t)row * o_nb2 + col_byte + rc * 16) = w;
+                }
+            };
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const bool mine = (l32 >> 4) == half;
+                if (o_type == KD_FA_TYPE_F32) {
+#pragma unroll
+                    for (int dblk = 0; dblk < 4; ++dblk) {
+                        if (mine) {
+#pragma unroll
+                            for (int g = 0; g < 4; ++g) {
+                                const f32x4 v = {o[dblk][4 * g] * inv, o[dblk][4 * g + 1] * inv,
+                                                 o[dblk][4 * g + 2] * inv, o[dblk][4 * g + 3] * inv};
+                                *reinterpret_cast<__attribute__((address_space(3))) f32x4 *>(
+                                    sO + r16 * 128 + (((2 * g + hi_b) ^ (r16 & 7)) << 4)) = v;
+                            }
+                        }
+                        flush(half, dblk * 128);
+                    }
+                } else {
+                    const bool bf = o_type == KD_FA_TYPE_BF16;
+#pragma unroll
+                    for (int rnd = 0; rnd < 2; ++rnd) {
+                        if (mine) {
+#pragma unroll
+                            for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+                                for (int g = 0; g < 4; ++g) {
+                                    const int dblk = 2 * rnd + dd;
+                                    const float v0 = o[dblk][4 * g] * inv, v1 = o[dblk][4 * g + 1] * inv;
+                                    const float v2 = o[dblk][4 * g + 2] * inv, v3 = o[dblk][4 * g + 3] * inv;
+                                    const u32x2 w = bf ? (u32x2){Elem<__bf16>::pack2(v0, v1), Elem<__bf16>::pack2(v2, v3)}
+                                                       : (u32x2){Elem<_Float16>::pack2(v0, v1), Elem<_Float16>::pack2(v2, v3)};
+                                    *reinterpret_cast<__attribute__((address_space(3))) u32x2 *>(
+                                        sO + r16 * 128 + (((dd * 4 + g) ^ (r16 & 7)) << 4) + 8 * hi_b) = w;
+                                }
+                        }
+                        flush(half, rnd * 128);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // fa_fwd_w64: the unmasked kernel with 64 query rows per wave.
 //
 // One workgroup = 4 waves = 256 query rows of one (batch, head), one wave per
@@ -911,6 +1366,27 @@ static hipError_t launch_w64_t(const Args &a, hipStream_t s) {
         hipLaunchKernelGGL((fa_fwd_w64<T, KD_FA_ROPE_NONE>), dim3(a.n_blocks), dim3(256), 0, s, a);
         break;
     }
+    return hipGetLastError();
+}
+
+template <typename T>
+static void launch_xres_t(const Args &a, hipStream_t s) {
+    const dim3 g(a.n_blocks), b(64 * kXWaves);
+    const bool q32 = a.q_type == KD_FA_TYPE_F32;
+    if (a.m) {
+        if (q32) hipLaunchKernelGGL((fa_fwd_xres<T, true, true>), g, b, 0, s, a);
+        else hipLaunchKernelGGL((fa_fwd_xres<T, true, false>), g, b, 0, s, a);
+    } else {
+        if (q32) hipLaunchKernelGGL((fa_fwd_xres<T, false, true>), g, b, 0, s, a);
+        else hipLaunchKernelGGL((fa_fwd_xres<T, false, false>), g, b, 0, s, a);
+    }
+}
+
+hipError_t launch_xres(const Args &a, int kv_type, hipStream_t s) {
+    if (kv_type == KD_FA_TYPE_BF16)
+        launch_xres_t<__bf16>(a, s);
+    else
+        launch_xres_t<_Float16>(a, s);
     return hipGetLastError();
 }
 
