@@ -13,8 +13,9 @@ Inputs are synthetic N(0,1) from a fixed seed and already resident in HBM.
 Prints ONE JSON line with the metric, the roofline of the attention kernel
 and a CPU baseline (the oracle's restatement of ggml's CPU algorithm on a
 bounded row sample, rank 0 only).  Secondary figures (the single-kernel
-kd_fa_rope_run, text cross-attention, the 60-layer step-equivalent) go in
-"secondary".
+kd_fa_rope_run, the 1,280- and 62,464-token self-attention, the text
+cross-attention, the VAE's D = 512 attention, the 60-layer step-equivalent)
+go in "secondary".
 """
 import argparse
 import json
@@ -39,7 +40,7 @@ def parse():
     p.add_argument("--rope", choices=["table", "axes"], default="table")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-secondary", action="store_true")
-    p.add_argument("--cpu-rows", type=int, default=3072, help="query rows per (b, h) in the CPU sample")
+    p.add_argument("--cpu-rows", type=int, default=2048, help="query rows per (b, h) in the CPU sample")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only copy 1 GiB device-to-device 3 times (scales the PMC byte counters)")
     return p.parse_args()
@@ -195,6 +196,27 @@ def main():
                              stream)
         sec["self_attn_norm_rope_ws_ms"] = round(ms_d, 4)
         sec["self_attn_norm_rope_ws_tflops"] = round(flop / (ms_d * 1e-3) / 1e12, 2)
+        # the other self-attention shapes, through the same kd_fa_rope_run_ws
+        # path: 1,280 tokens (f16, RoPE grid 5x16x16, batch 1; launch-bound)
+        # and 62,464 tokens (bf16, RoPE grid 61x32x32, batch 1)
+        for tag, (Bx, Tx, dt, seed) in (("c1_1280", (1, 5, torch.float16, 1)), ("c4_62464", (1, 61, bf, 4))):
+            Hx = 16 if tag.startswith("c1") else 32
+            Lx = Tx * Hx * Hx
+            qx = rand(torch, (Bx, HEADS, Lx, D), seed, dev, dt)
+            kx = rand(torch, (Bx, HEADS, Lx, D), seed + 1000, dev, dt)
+            vx = rand(torch, (Bx, HEADS, Lx, D), seed + 2000, dev, dt)
+            ox = torch.empty((Bx, Lx, HEADS, D), device=dev, dtype=torch.float32)
+            tx = kd_fa.visual_rope_table(Tx, Hx, Hx, AXES, SCALE_FACTOR, THETA)
+            ropex = kd_fa.rope_table(torch.from_numpy(tx).to(dev))
+            dx = kd_fa.make_desc(qx, kx, vx, None, ox, 1.0 / D ** 0.5)
+            wsx = torch.empty(kx.numel(), dtype=kx.dtype, device=dev)
+            n = 20 if tag.startswith("c1") else 3
+            msx = time_launches(torch, lambda: kd_fa.run_desc(dx, ropex, stream, wsx), n, 1, stream)
+            flx = 4.0 * Bx * HEADS * Lx * Lx * D
+            sec[f"self_attn_{tag}_ms"] = round(msx, 4)
+            sec[f"self_attn_{tag}_tflops"] = round(flx / (msx * 1e-3) / 1e12, 2)
+            sec[f"self_attn_{tag}_pct_bf16_peak"] = round(100.0 * flx / (msx * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2)
+            del qx, kx, vx, ox, wsx
         # text cross-attention: Q 31,744 x K/V 256, batch 2, padding mask 120 / 40 valid keys
         k2 = rand(torch, (B, HEADS, 256, D), 1002, dev, bf)
         v2 = rand(torch, (B, HEADS, 256, D), 2002, dev, bf)
