@@ -299,6 +299,10 @@ bool axes_ok(int T, int Hp, int Wp, const int axes[3]) {
 
 }  // namespace
 
+namespace kdfa {
+int device_gfx950() { return device_ok(); }
+}  // namespace kdfa
+
 extern "C" {
 
 int kd_fa_supports(const kd_fa_desc *desc, int *reason) {

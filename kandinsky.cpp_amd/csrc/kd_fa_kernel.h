@@ -47,6 +47,10 @@ struct Args {
     float norm_eps;
 };
 
+// KD_FA_OK when the current device is a gfx950 (checked once per device),
+// else KD_FA_ERR_DEVICE.
+int device_gfx950();
+
 // Enqueue the forward kernel for K/V element type kv_type on `stream`.
 // Q is normalised (qn_w) and rotated (RoPE mode) on load; K too (kn_w,
 // RoPE mode) when k_rope.
