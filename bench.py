@@ -14,8 +14,8 @@ Prints ONE JSON line with the metric, the roofline of the attention kernel
 and a CPU baseline (the oracle's restatement of ggml's CPU algorithm on a
 bounded row sample, rank 0 only).  Secondary figures (the single-kernel
 kd_fa_rope_run, the 1,280- and 62,464-token self-attention, the text
-cross-attention, the VAE's D = 512 attention, the 60-layer step-equivalent)
-go in "secondary".
+cross-attention, the VAE's D = 512 attention, the DiT linear layers through
+kd_mm_run, the 60-layer step-equivalent) go in "secondary".
 """
 import argparse
 import json
@@ -250,6 +250,34 @@ def main():
             sec[f"vae_attn_{L5}_ms"] = round(ms5v, 4)
             sec[f"vae_attn_{L5}_tflops"] = round(4.0 * L5 * L5 * 512 / (ms5v * 1e-3) / 1e12, 2)
             del q5, k5, v5, o5
+        # the DiT linear layers (ops::linear) at 63,488 tokens (31,744 x CFG 2):
+        # a 4096 x 4096 projection with Q8_0 weights expanded into the
+        # workspace on every call, the same with the weights kept as BF16 rows
+        # (F32 and BF16 activations), and the two feed-forward products
+        import kd_mm
+        Mx = B * L
+        wq8 = kd_mm.QuantWeight(torch.randint(0, 256, (4096, 4096 // 32 * 34), dtype=torch.uint8, device=dev),
+                                kd_mm.TYPE_Q8_0, 4096)
+        wq8.blocks.view(4096, 128, 34)[:, :, 1] = 0x20      # F16 scales of moderate size
+        for tag, (N_, K_, xdt, wkind) in (("qkv_q8_0_f32x", (4096, 4096, torch.float32, "q8")),
+                                          ("qkv_bf16w_f32x", (4096, 4096, torch.float32, "bf16")),
+                                          ("qkv_bf16w_bf16x", (4096, 4096, bf, "bf16")),
+                                          ("ffn_up_bf16w_f32x", (16384, 4096, torch.float32, "bf16")),
+                                          ("ffn_down_bf16w_f32x", (4096, 16384, torch.float32, "bf16"))):
+            xl = rand(torch, (Mx, K_), 51, dev, xdt)
+            yl = torch.empty((Mx, N_), device=dev, dtype=torch.float32)
+            bl = rand(torch, (N_,), 52, dev, torch.float32)
+            if wkind == "q8":
+                wl = wq8
+            else:
+                wl = rand(torch, (N_, K_), 53, dev, bf) * 0.05
+            dl = kd_mm.make_desc(wl, xl, bl, yl)
+            wsl = torch.empty(max(kd_mm.workspace_size(dl), 16), dtype=torch.uint8, device=dev)
+            msl = time_launches(torch, lambda: kd_mm.run_desc(dl, wsl, stream), 10, 2, stream)
+            fll = 2.0 * Mx * N_ * K_
+            sec[f"linear_{tag}_ms"] = round(msl, 4)
+            sec[f"linear_{tag}_tflops"] = round(fll / (msl * 1e-3) / 1e12, 2)
+            del xl, yl, wl, dl, wsl
         # 60 x (self + cross) with fresh buffers per layer (3 rotating sets)
         sets = [(q, k, v)] + [tuple(rand(torch, (B, HEADS, L, D), 10 * s + j, dev, bf) for j in range(3))
                               for s in range(1, 3)]

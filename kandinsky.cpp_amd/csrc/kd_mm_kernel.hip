@@ -111,20 +111,20 @@ hipError_t launch_dequant(const DqArgs &a, hipStream_t s) {
 // 256 (outputs) x 256 (tokens) tile of dst; wave w holds the 128 x 128
 // quarter (w & 1, w >> 1) as 4 x 4 MFMA accumulator blocks (256 AGPRs).
 //
-// K advances 32 per stage through three LDS stages, each filled by DMA
-// (global_load_lds_dwordx4) two stages ahead of its use:
+// K advances 32 per stage through S LDS stages (4 with BF16 X, 3 with F32
+// X: 128 / 144 KiB), each filled by DMA (global_load_lds_dwordx4) S - 1
+// stages ahead of its use:
 //   W stage: 256 rows x 64 bytes (BF16); 16-byte chunk c of row r at
-//            c ^ ((r >> 1) & 3)
+//            c ^ ((r >> 2) & 3)
 //   X stage: 256 rows x 128 bytes (F32) or 64 bytes (BF16); chunk c of row
-//            r at c ^ (r & 7) (F32) or c ^ ((r >> 1) & 3) (BF16)
-// -- so that the 32 rows an MFMA operand read touches spread over all
-// banks.  F32 X is rounded to BF16 as its fragments are read.  Per stage a
+//            r at c ^ ((r >> 1) & 7) (F32) or c ^ ((r >> 2) & 3) (BF16)
+// -- so that the 16 rows one 16-lane group of an operand read touches fill
+// the 256 bytes of the 64 banks exactly once.  F32 X is rounded to BF16 as its fragments are read.  Per stage a
 // wave reads 8 W and 8 X fragments and issues 32 MFMAs; the only barrier is
 // the one that publishes a stage.  Rows past M or N read clamped (repeated)
 // rows and are not stored; the workgroups of one row of tiles (all n tiles
 // of 256 tokens) run on one XCD, so its L2 serves their shared X stages.
 // ---------------------------------------------------------------------------
-constexpr int kMmStages = 3;
 constexpr int kMmWaves = 4;
 constexpr int kMmWTile = kMmBN * kMmBK * 2;   // 16 KiB
 
@@ -141,7 +141,9 @@ void mm_bf16(MmArgs a) {
     constexpr int kXRounds = kXTile / (kThreads * 16);     // 8 (F32) or 4
     constexpr int kWRowsPerRound = 1024 / 64;              // 16 rows per wave DMA
     constexpr int kXRowsPerRound = 1024 / kXRow;           // 8 or 16
-    __shared__ __attribute__((aligned(1024))) char lds[kMmStages * kStage];
+    constexpr int kS = XF32 ? 3 : 4;                       // LDS stages
+    constexpr int kPer = kWRounds + kXRounds;              // DMAs per stage per wave
+    __shared__ __attribute__((aligned(1024))) char lds[kS * kStage];
     lds_t *const sbase = LDS_PTR(char, lds);
 
     const int tid = threadIdx.x;
@@ -165,14 +167,14 @@ void mm_bf16(MmArgs a) {
 #pragma unroll
     for (int j = 0; j < kWRounds; ++j) {
         const int r = kWRowsPerRound * (wave + kMmWaves * j) + (lane >> 2);
-        const int c = (lane & 3) ^ ((r >> 1) & 3);
+        const int c = (lane & 3) ^ ((r >> 2) & 3);
         const int rr = n0 + r < a.N ? r : a.N - 1 - n0;
         w_off[j] = (uint32_t)rr * (uint32_t)a.w_nb1 + (uint32_t)(c << 4);
     }
 #pragma unroll
     for (int j = 0; j < kXRounds; ++j) {
         const int r = kXRowsPerRound * (wave + kMmWaves * j) + (XF32 ? (lane >> 3) : (lane >> 2));
-        const int c = XF32 ? ((lane & 7) ^ (r & 7)) : ((lane & 3) ^ ((r >> 1) & 3));
+        const int c = XF32 ? ((lane & 7) ^ ((r >> 1) & 7)) : ((lane & 3) ^ ((r >> 2) & 3));
         const int rr = m0 + r < a.M ? r : a.M - 1 - m0;
         x_off[j] = (uint32_t)rr * (uint32_t)a.x_nb1 + (uint32_t)(c << 4);
     }
@@ -196,12 +198,12 @@ void mm_bf16(MmArgs a) {
     uint32_t a_rd[2], b_rd[2][2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-        a_rd[ks] = (uint32_t)((128 * wn + l32) * 64 + (((2 * ks + hi) ^ ((l32 >> 1) & 3)) << 4));
+        a_rd[ks] = (uint32_t)((128 * wn + l32) * 64 + (((2 * ks + hi) ^ ((l32 >> 2) & 3)) << 4));
         if (XF32) {
-            b_rd[ks][0] = (uint32_t)(kMmWTile + (128 * wm + l32) * 128 + (((4 * ks + 2 * hi) ^ (l32 & 7)) << 4));
-            b_rd[ks][1] = (uint32_t)(kMmWTile + (128 * wm + l32) * 128 + (((4 * ks + 2 * hi + 1) ^ (l32 & 7)) << 4));
+            b_rd[ks][0] = (uint32_t)(kMmWTile + (128 * wm + l32) * 128 + (((4 * ks + 2 * hi) ^ ((l32 >> 1) & 7)) << 4));
+            b_rd[ks][1] = (uint32_t)(kMmWTile + (128 * wm + l32) * 128 + (((4 * ks + 2 * hi + 1) ^ ((l32 >> 1) & 7)) << 4));
         } else {
-            b_rd[ks][0] = (uint32_t)(kMmWTile + (128 * wm + l32) * 64 + (((2 * ks + hi) ^ ((l32 >> 1) & 3)) << 4));
+            b_rd[ks][0] = (uint32_t)(kMmWTile + (128 * wm + l32) * 64 + (((2 * ks + hi) ^ ((l32 >> 2) & 3)) << 4));
             b_rd[ks][1] = 0;
         }
     }
@@ -212,54 +214,87 @@ void mm_bf16(MmArgs a) {
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = (f32x16){};
 
-    auto compute = [&](int st) __attribute__((always_inline)) {
+    // operand fragments, two sets: the reads of one k-step are issued before
+    // the 16 MFMAs of the previous one, so their LDS latency hides behind
+    // 512 cycles of matrix work instead of stalling each group of four
+    vec8 fa0[4], fb0[4], fa1[4], fb1[4];
+    auto read = [&](int st, int ks, vec8 fa[4], vec8 fb[4]) __attribute__((always_inline)) {
         const lds_t *s = sbase + st * kStage;
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            vec8 af[4], bf[4];
+        for (int nb = 0; nb < 4; ++nb)
+            fa[nb] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(s + a_rd[ks] + nb * 32 * 64);
 #pragma unroll
-            for (int nb = 0; nb < 4; ++nb)
-                af[nb] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(s + a_rd[ks] + nb * 32 * 64);
-#pragma unroll
-            for (int mb = 0; mb < 4; ++mb) {
-                if constexpr (XF32) {
-                    const f32x4 u = *reinterpret_cast<const __attribute__((address_space(3))) f32x4 *>(
-                        s + b_rd[ks][0] + mb * 32 * 128);
-                    const f32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) f32x4 *>(
-                        s + b_rd[ks][1] + mb * 32 * 128);
-                    const u32x4 w = {E::pack2(u.x, u.y), E::pack2(u.z, u.w), E::pack2(v.x, v.y), E::pack2(v.z, v.w)};
-                    bf[mb] = __builtin_bit_cast(vec8, w);
-                } else {
-                    bf[mb] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(s + b_rd[ks][0] + mb * 32 * 64);
-                }
+        for (int mb = 0; mb < 4; ++mb) {
+            if constexpr (XF32) {
+                const f32x4 u = *reinterpret_cast<const __attribute__((address_space(3))) f32x4 *>(
+                    s + b_rd[ks][0] + mb * 32 * 128);
+                const f32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) f32x4 *>(
+                    s + b_rd[ks][1] + mb * 32 * 128);
+                const u32x4 w = {E::pack2(u.x, u.y), E::pack2(u.z, u.w), E::pack2(v.x, v.y), E::pack2(v.z, v.w)};
+                fb[mb] = __builtin_bit_cast(vec8, w);
+            } else {
+                fb[mb] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(s + b_rd[ks][0] + mb * 32 * 64);
             }
-#pragma unroll
-            for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-                for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = E::mfma(af[nb], bf[mb], acc[nb][mb]);
         }
     };
-
-    const int nk = a.K / kMmBK;
-    issue(0, 0);
-    if (nk > 1) issue(1, 1);
-    int st = 0;
-    for (int kt = 0; kt < nk; ++kt) {
-        // this stage's DMA done (the next stage's may still be in flight)
-        if (kt + 1 < nk) {
-            if constexpr (XF32)
-                asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
-            else
-                asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-        } else {
+    auto mfmas = [&](const vec8 fa[4], const vec8 fb[4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = E::mfma(fa[nb], fb[mb], acc[nb][mb]);
+    };
+    // a stage is complete in LDS for every wave: this wave's DMAs of it have
+    // landed (the `later` stages issued after it may be in flight; DMAs
+    // complete in issue order), then the barrier
+    auto publish = [&](int later) __attribute__((always_inline)) {
+        static_assert(3 * kPer <= 63, "vmcnt range");
+        if (later >= 3)
+            asm volatile("s_waitcnt vmcnt(%0)" :: "n"(3 * kPer) : "memory");
+        else if (later == 2)
+            asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * kPer) : "memory");
+        else if (later == 1)
+            asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kPer) : "memory");
+        else
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        }
         __syncthreads();
-        if (kt + 2 < nk) issue(kt + 2, st == 0 ? 2 : st - 1);
-        compute(st);
-        st = st == 2 ? 0 : st + 1;
+    };
+
+    // Step kt (stage st = kt % S): start the DMA of stage kt+S-1; 16 MFMAs of
+    // k-step 0 while the fragments of k-step 1 load; publish stage kt+1 (its
+    // DMAs landed, later stages' may be in flight); 16 MFMAs of k-step 1
+    // while the fragments of stage kt+1's k-step 0 load.
+    constexpr int kLead = kS - 1;
+    const int nk = a.K / kMmBK;
+#pragma unroll
+    for (int j = 0; j < kLead; ++j)
+        if (j < nk) issue(j, j);
+    publish(min(kLead, nk) - 1);
+    read(0, 0, fa0, fb0);
+    int st = 0;
+    // The last step is peeled so that every step of the loop issues the same
+    // LDS reads (a read under a branch makes the wait counts conservative);
+    // sched_barrier keeps the compiler from moving reads next to their uses.
+    for (int kt = 0; kt + 1 < nk; ++kt) {
+        const int st1 = st == kS - 1 ? 0 : st + 1;
+        // stage kt+S-1 goes into the buffer of stage kt-1, whose reads all
+        // completed before the previous barrier (its fence drains them)
+        if (kt + kLead < nk) issue(kt + kLead, st == 0 ? kS - 1 : st - 1);
+        read(st, 1, fa1, fb1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(fa0, fb0);
+        __builtin_amdgcn_sched_barrier(0);
+        publish(min(kLead, nk - 1 - kt) - 1);
+        read(st1, 0, fa0, fb0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(fa1, fb1);
+        __builtin_amdgcn_sched_barrier(0);
+        st = st1;
     }
-    static_assert(kWRounds + kXRounds == (XF32 ? 12 : 8), "per-stage DMA count");
+    read(st, 1, fa1, fb1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(fa0, fb0);
+    mfmas(fa1, fb1);
+    static_assert(kPer == (XF32 ? 12 : 8), "per-stage DMA count");
 
     // ---- epilogue: dst[m][n .. n+3] = acc (+ bias) ----------------------------
 #pragma unroll
