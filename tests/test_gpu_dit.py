@@ -15,7 +15,7 @@ import torch
 
 import kd_fa
 import kd_oracle as orc
-from fa_common import AXES, D, SCALE_FACTOR, THETA, assert_parity, gather_rows, padding_mask, qkv, randn
+from fa_common import AXES, D, SCALE_FACTOR, THETA, assert_parity, gather_rows, padding_mask, qkv, randn, sample_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -83,6 +83,34 @@ def test_self_attention_norm_rope(dt):
     assert torch.equal(fused, _plain(q2, k2, v))
     ref = orc.fa_f64(q2, k2, v)
     assert_parity(gather_rows(fused, np.arange(B * H * L), H, L), ref, "dit self-attention")
+
+
+@pytest.mark.parametrize("L", [77, 256, 300])
+def test_text_block_self_attention(L):
+    """TextBlock self-attention (src/models/crossdit.hpp:234-275): the same
+    DiTSelfAttention with the 1-D text RoPE table (rope::compute_text_rope,
+    src/rope.hpp:36-49, built at crossdit.hpp:562) over the prompt tokens,
+    CFG batch 2, 32 heads; fused and workspace forms bitwise equal, both equal
+    to the plain node on the oracle-transformed operands."""
+    _need_gpu()
+    _announce(f"text block self-attention L={L}")
+    B, H = 2, 32
+    q, k, v = qkv(B, H, L, L, torch.bfloat16, seed=L, q_dtype=torch.float32)
+    wq, wk = _weights(L + 1)
+    table = kd_fa.text_rope_table(L, D)
+    norm = kd_fa.qk_norm(wq.to(DEV), wk.to(DEV), EPS)
+    rope = kd_fa.rope_table(torch.from_numpy(table).to(DEV))
+    qg, kg, vg = q.to(DEV), k.to(DEV), v.to(DEV)
+    fused = kd_fa.flash_attn_ext(qg, kg, vg, rope=rope, norm=norm)
+    ws = torch.empty(k.numel(), dtype=torch.bfloat16, device=DEV)
+    viaws = kd_fa.flash_attn_ext(qg, kg, vg, rope=rope, norm=norm, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, viaws)
+    q2 = _rot(_norm(q, wq), table, torch.bfloat16)
+    k2 = _rot(_norm(k, wk), table, torch.bfloat16)
+    assert torch.equal(fused, _plain(q2, k2, v))
+    rows = sample_rows(B, H, L, 32, seed=L + 2)
+    assert_parity(gather_rows(fused, rows, H, L), orc.fa_f64(q2, k2, v, rows=rows), "text block")
 
 
 def test_self_attention_f32_k_through_workspace():
