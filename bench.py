@@ -43,6 +43,8 @@ def parse():
     p.add_argument("--cpu-rows", type=int, default=2048, help="query rows per (b, h) in the CPU sample")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only copy 1 GiB device-to-device 3 times (scales the PMC byte counters)")
+    p.add_argument("--cross-only", action="store_true",
+                   help="only the text cross-attention (C2 shape): for counter runs of its kernel")
     return p.parse_args()
 
 
@@ -126,6 +128,18 @@ def main():
     B, T, Hp, Wp = 2, 31, 32, 32
     L = T * Hp * Wp
     bf = torch.bfloat16
+    if args.cross_only:
+        qx = rand(torch, (B, HEADS, L, D), 3, dev, bf)
+        kx = rand(torch, (B, HEADS, 256, D), 1002, dev, bf)
+        vx = rand(torch, (B, HEADS, 256, D), 2002, dev, bf)
+        mx = torch.full((B, 1, L, 256), float("-inf"), dtype=torch.float16, device=dev)
+        mx[0, :, :, :120] = 0
+        mx[1, :, :, :40] = 0
+        ox = torch.empty((B, L, HEADS, D), device=dev, dtype=torch.float32)
+        dx = kd_fa.make_desc(qx, kx, vx, mx, ox, 1.0 / D ** 0.5)
+        msx = time_launches(torch, lambda: kd_fa.run_desc(dx, None, stream), args.steps, args.warmup, stream)
+        print(json.dumps({"cross_attn_ms": round(msx, 4)}))
+        return
     q = rand(torch, (B, HEADS, L, D), 3, dev, bf)
     k = rand(torch, (B, HEADS, L, D), 1003, dev, bf)
     v = rand(torch, (B, HEADS, L, D), 2003, dev, bf)
