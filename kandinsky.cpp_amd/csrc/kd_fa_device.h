@@ -246,4 +246,36 @@ static __device__ __forceinline__ double sum16_f64(double x) {
     return x;
 }
 
+// O / l of query row q_row -> dst[b][q_row][h][d_base + :128] (F32, or
+// rounded to F16 / BF16).  o holds O^T of the row's 32-row block in MFMA
+// accumulator order (element i of d block dblk: d = dblk*32 + 8*(i/4) +
+// 4*hi + i%4); l_run is the row's weight sum (the kernels that hold half of
+// it per lane add the lane pair first).
+static __device__ __forceinline__ void store_o_row_l(const Args &a, int q_row, int h, int b, int hi, const f32x16 o[4],
+                                              float l_run, int d_base) {
+    if (q_row < a.Lq) {
+        const float inv = l_run == 0.0f ? 0.0f : 1.0f / l_run;
+        char *op = a.o + (int64_t)b * a.o_nb3 + (int64_t)q_row * a.o_nb2 + (int64_t)h * a.o_nb1 +
+                   (int64_t)d_base * (a.o_type == KD_FA_TYPE_F32 ? 4 : 2);
+        const int ot = a.o_type;
+#pragma unroll
+        for (int dblk = 0; dblk < 4; ++dblk)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = dblk * 32 + 8 * g + 4 * hi;
+                const f32x4 v = {o[dblk][4 * g] * inv, o[dblk][4 * g + 1] * inv,
+                                 o[dblk][4 * g + 2] * inv, o[dblk][4 * g + 3] * inv};
+                if (ot == KD_FA_TYPE_F32) {
+                    *reinterpret_cast<f32x4 *>(op + d * 4) = v;
+                } else if (ot == KD_FA_TYPE_BF16) {
+                    const u32x2 w = {Elem<__bf16>::pack2(v.x, v.y), Elem<__bf16>::pack2(v.z, v.w)};
+                    *reinterpret_cast<u32x2 *>(op + d * 2) = w;
+                } else {
+                    const u32x2 w = {Elem<_Float16>::pack2(v.x, v.y), Elem<_Float16>::pack2(v.z, v.w)};
+                    *reinterpret_cast<u32x2 *>(op + d * 2) = w;
+                }
+            }
+    }
+}
+
 }  // namespace kdfa

@@ -252,9 +252,14 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
     }
     hipStream_t hs = static_cast<hipStream_t>(stream);
     if (d->q.ne[0] == kHeadDimVae) {
-        a.n_qt = (int32_t)((Lq + 31) / 32);
+        // 64 query rows per workgroup (half the key stream per row) when that
+        // still gives every CU a workgroup, else 32; KD_FA_D512_ROWS=32 in the
+        // environment forces 32 (for comparisons)
+        const char *e = std::getenv("KD_FA_D512_ROWS");
+        const int rows = ((e && std::atoi(e) == 32) || (Lq + 63) / 64 * H * B < 256) ? 32 : 64;
+        a.n_qt = (int32_t)((Lq + rows - 1) / rows);
         a.n_blocks = (int32_t)(a.n_qt * H * B);
-        return kdfa::launch_d512(a, d->v.type, hs) == hipSuccess ? KD_FA_OK : KD_FA_ERR_LAUNCH;
+        return kdfa::launch_d512(a, d->v.type, rows, hs) == hipSuccess ? KD_FA_OK : KD_FA_ERR_LAUNCH;
     }
     bool k_rope = k_xform && !ws;
     const int rows = kdfa::block_rows(a.m != nullptr, k_rope);

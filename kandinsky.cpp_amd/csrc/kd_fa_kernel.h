@@ -67,7 +67,9 @@ constexpr int kXresMaxKeys = 256;
 hipError_t launch_xres(const Args &a, int kv_type, hipStream_t stream);
 
 // Enqueue the D = 512 kernel (no mask, no RoPE; 32-row query tiles).
-hipError_t launch_d512(const Args &a, int kv_type, hipStream_t stream);
+// rows: query rows per workgroup, 32 or 64 (a.n_qt and a.n_blocks counted in
+// those)
+hipError_t launch_d512(const Args &a, int kv_type, int rows, hipStream_t stream);
 
 // Normalise (kn_w) and rotate (RoPE mode) K ([D, Lk, H/rk2, B/rk3] through
 // a.k and its strides) into `out`, contiguous, in K's type.

@@ -147,38 +147,6 @@ __device__ __forceinline__ void load_q_frags(const Args &a, int q_ld, int h, int
     }
 }
 
-// O / l of query row q_row -> dst[b][q_row][h][d_base + :128] (F32, or
-// rounded to F16 / BF16).  o holds O^T of the row's 32-row block in MFMA
-// accumulator order (element i of d block dblk: d = dblk*32 + 8*(i/4) +
-// 4*hi + i%4); l_run is the row's weight sum (store_o_row: this lane's
-// half of it, the other half in lane l ^ 32).
-__device__ __forceinline__ void store_o_row_l(const Args &a, int q_row, int h, int b, int hi, const f32x16 o[4],
-                                              float l_run, int d_base) {
-    if (q_row < a.Lq) {
-        const float inv = l_run == 0.0f ? 0.0f : 1.0f / l_run;
-        char *op = a.o + (int64_t)b * a.o_nb3 + (int64_t)q_row * a.o_nb2 + (int64_t)h * a.o_nb1 +
-                   (int64_t)d_base * (a.o_type == KD_FA_TYPE_F32 ? 4 : 2);
-        const int ot = a.o_type;
-#pragma unroll
-        for (int dblk = 0; dblk < 4; ++dblk)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int d = dblk * 32 + 8 * g + 4 * hi;
-                const f32x4 v = {o[dblk][4 * g] * inv, o[dblk][4 * g + 1] * inv,
-                                 o[dblk][4 * g + 2] * inv, o[dblk][4 * g + 3] * inv};
-                if (ot == KD_FA_TYPE_F32) {
-                    *reinterpret_cast<f32x4 *>(op + d * 4) = v;
-                } else if (ot == KD_FA_TYPE_BF16) {
-                    const u32x2 w = {Elem<__bf16>::pack2(v.x, v.y), Elem<__bf16>::pack2(v.z, v.w)};
-                    *reinterpret_cast<u32x2 *>(op + d * 2) = w;
-                } else {
-                    const u32x2 w = {Elem<_Float16>::pack2(v.x, v.y), Elem<_Float16>::pack2(v.z, v.w)};
-                    *reinterpret_cast<u32x2 *>(op + d * 2) = w;
-                }
-            }
-    }
-}
-
 __device__ __forceinline__ void store_o_row(const Args &a, int q_row, int h, int b, int hi, const f32x16 o[4],
                                             float l_half) {
     store_o_row_l(a, q_row, h, b, hi, o, pair_sum(l_half), 0);
@@ -1485,211 +1453,6 @@ hipError_t launch_rope_k(const Args &a, int kv_type, int k_heads, int k_batch, v
     else
         launch_rope_k_t<_Float16>(a, grid, o, n_chunks, stream);
     return hipGetLastError();
-}
-
-
-// ---------------------------------------------------------------------------
-// fa_fwd_d512: the attention of the 2-D VAE's attention block
-// (src/models/vae.hpp:60-101 -> ops::attention with one head, D = channels =
-// 512), no mask, no RoPE.
-//
-// A workgroup is 4 waves and covers 32 query rows of one (b, h); wave w owns
-// the 128 columns 128w .. 128w+127 of D for both products, so that its O
-// (32 rows x 128) and Q (32 rows x 128) stay in registers.  Per 32-key tile:
-//   S_w^T = K_w Q_w^T over the wave's 128 columns (8 MFMA), K fragments
-//           straight from global memory (each wave reads only its columns);
-//   the four partial scores meet in LDS; wave w runs the online softmax of
-//           rows 8w .. 8w+7 (exact running max, exp2 domain) and writes the
-//           weights P (rounded to the operand type), the rescale factor and,
-//           at the end, the row sum to LDS for all waves;
-//   O_w^T = alpha * O_w^T + V_w^T P^T (8 MFMA), V_w staged by DMA in the
-//           wave's own LDS region (double-buffered, no barrier: only that
-//           wave reads it) and read transposed with ds_read_b64_tr_b16.
-// Two barriers per tile.  Keys past Lk (last tile) load clamped rows and get
-// weight 0.
-constexpr int kD5 = 512;                     // D, four 128-column slices
-constexpr int kD5Keys = 32;                    // keys per tile
-constexpr int kD5Rows = 32;                    // query rows per workgroup
-constexpr int kD5SStride = kD5Keys + 4;        // floats per row of a partial-score block (pad)
-constexpr int kD5PStride = kD5Keys + 8;        // 16-bit weights per row of P (pad)
-constexpr int kD5VTile = kD5Keys * 256;        // one wave's V tile: 32 keys x 128 columns
-
-static_assert(kD5 == 4 * 128, "one 128-column slice per wave");
-
-template <typename T>
-__global__ __launch_bounds__(256) void fa_fwd_d512(Args a) {
-    typedef Elem<T> E;
-    typedef typename E::vec8 vec8;
-    __shared__ __attribute__((aligned(16))) float sS[4][kD5Rows][kD5SStride];
-    __shared__ __attribute__((aligned(16))) uint16_t sP[kD5Rows][kD5PStride];
-    __shared__ float sAlpha[kD5Rows];
-    __shared__ float sL[kD5Rows];
-    __shared__ __attribute__((aligned(1024))) char sV[4][2][kD5VTile];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int l32 = lane & 31;
-    const int hi = lane >> 5;
-    const int qt = blockIdx.x % a.n_qt;
-    const int bh = blockIdx.x / a.n_qt;
-    const int h = bh % a.H;
-    const int b = bh / a.H;
-    const int Lk = a.Lk;
-    const int n_tiles = (Lk + kD5Keys - 1) / kD5Keys;
-    const int col0 = 128 * wave;                  // this wave's columns of D
-
-    // Q fragments of the wave's columns (B operands of S_w^T = K_w Q_w^T)
-    const int q_row = qt * kD5Rows + l32;
-    const int q_ld = q_row < a.Lq ? q_row : a.Lq - 1;
-    vec8 qf[8];
-    {
-        const char *qp = a.q + (int64_t)q_ld * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)b * a.q_nb3;
-        const int esz = a.q_type == KD_FA_TYPE_F32 ? 4 : 2;
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-            float x[8];
-            load8_f32(qp + (col0 + ks * 16 + hi * 8) * esz, a.q_type, x);
-            u32x4 w;
-            for (int j = 0; j < 4; ++j) w[j] = E::pack2(x[2 * j], x[2 * j + 1]);
-            if (a.scale_log2 < 0.0f) w ^= (u32x4){0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
-            qf[ks] = __builtin_bit_cast(vec8, w);
-        }
-    }
-    const float c2 = __builtin_fabsf(a.scale_log2);
-
-    const char *kbase = a.k + (int64_t)(h / a.rk2) * a.k_nb2 + (int64_t)(b / a.rk3) * a.k_nb3 + col0 * 2;
-    const char *vbase = a.v + (int64_t)(h / a.rv2) * a.v_nb2 + (int64_t)(b / a.rv3) * a.v_nb3 + col0 * 2;
-    // K fragment of k-step ks: key (tile row) l32, columns ks*16 + hi*8 .. +7
-    auto load_k = [&](int t, vec8 kf[8]) __attribute__((always_inline)) {
-        int key = t * kD5Keys + l32;
-        key = key < Lk ? key : Lk - 1;
-        const char *kp = kbase + (int64_t)key * a.k_nb1 + hi * 16;
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) kf[ks] = __builtin_bit_cast(vec8, ld16(kp + ks * 32));
-    };
-    // V tile of this wave: LDS row r (key t*32 + r, clamped) holds the wave's
-    // 128 columns, 16-byte chunk c at c ^ v_swz(r); 8 DMA rounds of 4 rows
-    const int dma_row = lane >> 4, dma_pc = lane & 15;
-    auto issue_v = [&](int t, int buf) __attribute__((always_inline)) {
-        lds_t *dst = LDS_PTR(char, sV[wave][buf]);
-#pragma unroll
-        for (int j = 0; j < kD5Keys / 4; ++j) {
-            const int r = 4 * j + dma_row;
-            int key = t * kD5Keys + r;
-            key = key < Lk ? key : Lk - 1;
-            dma16(vbase, (uint32_t)key * (uint32_t)a.v_nb1 + ((dma_pc ^ v_swz(r)) << 4), dst + j * 1024);
-        }
-    };
-    const int v_sub = (lane & 15) >> 2;
-    const int v_c_lo = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
-    uint32_t v_rd[4];
-#pragma unroll
-    for (int dblk = 0; dblk < 4; ++dblk)
-        v_rd[dblk] = 2048 * hi + 256 * v_sub + (((4 * dblk + v_c_lo) ^ v_swz(v_sub)) << 4) + 8 * (lane & 1);
-
-    f32x16 o[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = (f32x16){};
-    // softmax state of row 8*wave + lane/8 (the 8 lanes of a row agree)
-    const int srow = 8 * wave + (lane >> 3);
-    const int skey = 4 * (lane & 7);
-    float m_run = -INFINITY, l_run = 0.0f;
-
-    // VMEM order per tile: the V DMA (inline asm, invisible to the
-    // compiler's vmcnt bookkeeping) before the K loads, so that the
-    // compiler's own waits for K stay exact (loads complete in order) and
-    // V(t) has landed once at most the 16 newer loads are in flight
-    vec8 kf[8];
-    if (n_tiles > 0) {
-        issue_v(0, 0);
-        load_k(0, kf);
-    }
-    for (int t = 0; t < n_tiles; ++t) {
-        // ---- partial scores over this wave's columns
-        f32x16 s = (f32x16){};
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) s = E::mfma(kf[ks], qf[ks], s);
-        if (t + 1 < n_tiles) {
-            issue_v(t + 1, (t + 1) & 1);
-            load_k(t + 1, kf);
-        }
-        // element i of lane l: key 8*(i/4) + 4*hi + i%4, query l32
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-            *reinterpret_cast<f32x4 *>(&sS[wave][l32][8 * g + 4 * hi]) =
-                (f32x4){s[4 * g], s[4 * g + 1], s[4 * g + 2], s[4 * g + 3]};
-        __syncthreads();
-        // ---- softmax of rows 8w .. 8w+7: 4 keys per lane
-        {
-            f32x4 x = *reinterpret_cast<const f32x4 *>(&sS[0][srow][skey]);
-#pragma unroll
-            for (int w = 1; w < 4; ++w)
-                x += *reinterpret_cast<const f32x4 *>(&sS[w][srow][skey]);
-            float sc[4] = {x.x * c2, x.y * c2, x.z * c2, x.w * c2};
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (t * kD5Keys + skey + e >= Lk) sc[e] = -INFINITY;
-            float mx = __builtin_fmaxf(__builtin_fmaxf(sc[0], sc[1]), __builtin_fmaxf(sc[2], sc[3]));
-            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 1));
-            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 2));
-            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 4));
-            const float m_new = __builtin_fmaxf(m_run, mx);
-            const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-            m_run = m_new;
-            const float mu = m_new == -INFINITY ? 0.0f : m_new;
-            float p[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(sc[e] - mu);
-            float ps = (p[0] + p[1]) + (p[2] + p[3]);
-            ps += __shfl_xor(ps, 1);
-            ps += __shfl_xor(ps, 2);
-            ps += __shfl_xor(ps, 4);
-            l_run = l_run * alpha + ps;
-            const u32x2 w = {E::pack2(p[0], p[1]), E::pack2(p[2], p[3])};
-            *reinterpret_cast<u32x2 *>(&sP[srow][skey]) = w;
-            if ((lane & 7) == 0) sAlpha[srow] = alpha;
-        }
-        __syncthreads();
-        // ---- O_w^T = alpha * O_w^T + V_w^T P^T
-        const float al = sAlpha[l32];
-        if (__builtin_amdgcn_ballot_w64(al != 1.0f) != 0) {
-#pragma unroll
-            for (int dblk = 0; dblk < 4; ++dblk)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) o[dblk][i] *= al;
-        }
-        if (t + 1 < n_tiles)
-            asm volatile("s_waitcnt vmcnt(16)" ::: "memory");   // V(t) landed; V(t+1), K(t+1) may fly
-        else
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        const lds_t *vs_ = LDS_PTR(char, sV[wave][t & 1]);
-#pragma unroll
-        for (int kst = 0; kst < kD5Keys / 16; ++kst) {
-            const vec8 pb = *reinterpret_cast<const vec8 *>(&sP[l32][16 * kst + 8 * hi]);
-#pragma unroll
-            for (int dblk = 0; dblk < 4; ++dblk) {
-                const lds_t *vp = vs_ + v_rd[dblk] + 4096 * kst;
-                const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(vp));
-                const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(vp + 1024));
-                const vec8 va = __builtin_bit_cast(vec8, __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
-                o[dblk] = E::mfma(va, pb, o[dblk]);
-            }
-        }
-    }
-    if ((lane & 7) == 0) sL[srow] = l_run;
-    __syncthreads();
-    store_o_row_l(a, q_row, h, b, hi, o, sL[l32], col0);
-}
-
-template <typename T>
-static hipError_t launch_d512_t(const Args &a, hipStream_t s) {
-    hipLaunchKernelGGL((fa_fwd_d512<T>), dim3(a.n_blocks), dim3(256), 0, s, a);
-    return hipGetLastError();
-}
-
-hipError_t launch_d512(const Args &a, int kv_type, hipStream_t stream) {
-    return kv_type == KD_FA_TYPE_BF16 ? launch_d512_t<__bf16>(a, stream) : launch_d512_t<_Float16>(a, stream);
 }
 
 }  // namespace kdfa

@@ -15,6 +15,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/kd_mm.h"
 #include "kd_fa_device.h"
 #include "kd_mm_kernel.h"
@@ -216,9 +218,15 @@ void mm_bf16(MmArgs a) {
 
     // operand fragments, two sets: the reads of one k-step are issued before
     // the 16 MFMAs of the previous one, so their LDS latency hides behind
-    // 512 cycles of matrix work instead of stalling each group of four
-    vec8 fa0[4], fb0[4], fa1[4], fb1[4];
-    auto read = [&](int st, int ks, vec8 fa[4], vec8 fb[4]) __attribute__((always_inline)) {
+    // 512 cycles of matrix work instead of stalling each group of four.  F32
+    // X fragments are kept as read and rounded to BF16 next to the products
+    // that use them, so that no rounding waits on a read just issued.
+    struct XFragBf16 { vec8 b[4]; };
+    struct XFragF32 { f32x4 u[4], v[4]; };
+    typedef typename std::conditional<XF32, XFragF32, XFragBf16>::type XFrag;
+    vec8 fa0[4], fa1[4];
+    XFrag fb0, fb1;
+    auto read = [&](int st, int ks, vec8 fa[4], XFrag &fb) __attribute__((always_inline)) {
         const lds_t *s = sbase + st * kStage;
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb)
@@ -226,22 +234,27 @@ void mm_bf16(MmArgs a) {
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
             if constexpr (XF32) {
-                const f32x4 u = *reinterpret_cast<const __attribute__((address_space(3))) f32x4 *>(
-                    s + b_rd[ks][0] + mb * 32 * 128);
-                const f32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) f32x4 *>(
-                    s + b_rd[ks][1] + mb * 32 * 128);
-                const u32x4 w = {E::pack2(u.x, u.y), E::pack2(u.z, u.w), E::pack2(v.x, v.y), E::pack2(v.z, v.w)};
-                fb[mb] = __builtin_bit_cast(vec8, w);
+                fb.u[mb] = *reinterpret_cast<const __attribute__((address_space(3))) f32x4 *>(s + b_rd[ks][0] + mb * 32 * 128);
+                fb.v[mb] = *reinterpret_cast<const __attribute__((address_space(3))) f32x4 *>(s + b_rd[ks][1] + mb * 32 * 128);
             } else {
-                fb[mb] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(s + b_rd[ks][0] + mb * 32 * 64);
+                fb.b[mb] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(s + b_rd[ks][0] + mb * 32 * 64);
             }
         }
     };
-    auto mfmas = [&](const vec8 fa[4], const vec8 fb[4]) __attribute__((always_inline)) {
+    auto mfmas = [&](const vec8 fa[4], const XFrag &fb) __attribute__((always_inline)) {
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
+        for (int mb = 0; mb < 4; ++mb) {
+            vec8 b;
+            if constexpr (XF32) {
+                const f32x4 u = fb.u[mb], v = fb.v[mb];
+                const u32x4 w = {E::pack2(u.x, u.y), E::pack2(u.z, u.w), E::pack2(v.x, v.y), E::pack2(v.z, v.w)};
+                b = __builtin_bit_cast(vec8, w);
+            } else {
+                b = fb.b[mb];
+            }
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = E::mfma(fa[nb], fb[mb], acc[nb][mb]);
+            for (int nb = 0; nb < 4; ++nb) acc[nb][mb] = E::mfma(fa[nb], b, acc[nb][mb]);
+        }
     };
     // a stage is complete in LDS for every wave: this wave's DMAs of it have
     // landed (the `later` stages issued after it may be in flight; DMAs
@@ -297,22 +310,44 @@ void mm_bf16(MmArgs a) {
     static_assert(kPer == (XF32 ? 12 : 8), "per-stage DMA count");
 
     // ---- epilogue: dst[m][n .. n+3] = acc (+ bias) ----------------------------
+    // Through LDS, one 32-output block (128 bytes of each of the wave's 128
+    // token rows) at a time: the lanes leave their 16-byte pieces in the
+    // wave's own 16 KiB (chunk index XOR (row >> 1) & 7: no bank conflicts),
+    // then lane L reads chunk L % 8 of row 8j + L / 8, so that every store
+    // instruction writes eight whole 128-byte lines of dst instead of
+    // 32-byte pieces of 32 rows.  The stage buffers are free once every wave
+    // is past its last read; after that a wave touches only its own region
+    // (its LDS operations complete in order).
+    __syncthreads();
+    lds_t *const sO = sbase + wave * 32768;
+    const int rr = lane >> 3;
+    const int rc = lane & 7;
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
+        lds_t *const so = sO + (nb & 1) * 16384;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int n = n0 + 128 * wn + 32 * nb + 8 * g + 4 * hi;
-            if (n >= a.N) continue;
-            f32x4 bias = {0.f, 0.f, 0.f, 0.f};
-            if (a.bias) bias = *reinterpret_cast<const f32x4 *>(a.bias + n);
+        for (int mb = 0; mb < 4; ++mb) {
+            const int row = 32 * mb + l32;
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb) {
-                const int m = m0 + 128 * wm + 32 * mb + l32;
-                if (m < a.M) {
-                    const f32x4 v = {acc[nb][mb][4 * g] + bias.x, acc[nb][mb][4 * g + 1] + bias.y,
-                                     acc[nb][mb][4 * g + 2] + bias.z, acc[nb][mb][4 * g + 3] + bias.w};
-                    *reinterpret_cast<f32x4 *>(a.dst + (int64_t)m * a.d_nb1 + (int64_t)n * 4) = v;
-                }
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 v = {acc[nb][mb][4 * g], acc[nb][mb][4 * g + 1], acc[nb][mb][4 * g + 2],
+                                 acc[nb][mb][4 * g + 3]};
+                *reinterpret_cast<__attribute__((address_space(3))) f32x4 *>(
+                    so + row * 128 + (((2 * g + hi) ^ ((row >> 1) & 7)) << 4)) = v;
+            }
+        }
+        const int n = n0 + 128 * wn + 32 * nb + 4 * rc;
+        f32x4 bias = {0.f, 0.f, 0.f, 0.f};
+        if (a.bias && n < a.N) bias = *reinterpret_cast<const f32x4 *>(a.bias + n);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int row = 8 * j + rr;
+            f32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) f32x4 *>(
+                so + row * 128 + ((rc ^ ((row >> 1) & 7)) << 4));
+            const int m = m0 + 128 * wm + row;
+            if (m < a.M && n < a.N) {
+                v.x += bias.x; v.y += bias.y; v.z += bias.z; v.w += bias.w;
+                *reinterpret_cast<f32x4 *>(a.dst + (int64_t)m * a.d_nb1 + (int64_t)n * 4) = v;
             }
         }
     }

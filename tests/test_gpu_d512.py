@@ -100,3 +100,55 @@ def test_d512_vae_64x64_sampled():
     out = _run(q, k, v, scale=D ** -0.5)
     rows = sample_rows(1, 1, L, 64, seed=32)
     assert_parity(gather_rows(out, rows, 1, L), orc.fa_f64(q, k, v, scale=D ** -0.5, rows=rows), "d512 4096")
+
+
+def _run_rows32(q, k, v, **kw):
+    """The same call with 32 query rows per workgroup forced."""
+    import os
+    old = os.environ.get("KD_FA_D512_ROWS")
+    os.environ["KD_FA_D512_ROWS"] = "32"
+    try:
+        return _run(q, k, v, **kw)
+    finally:
+        if old is None:
+            del os.environ["KD_FA_D512_ROWS"]
+        else:
+            os.environ["KD_FA_D512_ROWS"] = old
+
+
+ROWS64_CASES = [
+    # B, H, Hkv, Bk, Lq, Lk, K/V type: >= 256 workgroups of 64 rows, so the
+    # 64-row kernel runs; ragged query blocks (Lq % 64) and key tiles
+    (4, 64, 64, 4, 100, 45, torch.float16),
+    (2, 128, 32, 1, 64, 97, torch.bfloat16),
+    (1, 256, 256, 1, 33, 32, torch.float16),
+]
+
+
+@pytest.mark.parametrize("case", ROWS64_CASES, ids=lambda c: f"B{c[0]}H{c[1]}kv{c[2]}q{c[4]}k{c[5]}")
+def test_d512_64_rows_equal_32_rows(case):
+    """Two 32-row blocks per wave (the key stream shared by 64 rows) give
+    bitwise the 32-row kernel's result; both agree with the oracle."""
+    _need_gpu()
+    B, H, Hkv, Bk, Lq, Lk, kt = case
+    _announce(f"d512 64 rows {case}")
+    q, k, v = _qkv(B, H, Lq, Lk, kt, seed=Lq + Lk + H, Hkv=Hkv, Bk=Bk)
+    scale = D ** -0.5
+    out = _run(q, k, v, scale=scale)
+    assert torch.equal(out, _run_rows32(q, k, v, scale=scale))
+    rows = sample_rows(B, H, Lq, 48, seed=Lk)
+    assert_parity(gather_rows(out, rows, H, Lq), orc.fa_f64(q, k, v, scale=scale, rows=rows), f"d512 64 rows {case}")
+
+
+def test_d512_vae_128x128_sampled():
+    """The mid-block attention at a 128x128 latent (1024-pixel images):
+    16,384 tokens, one head -- 256 workgroups of 64 rows; bitwise the 32-row
+    kernel's result, sampled rows against the oracle."""
+    _need_gpu()
+    _announce("d512 16384 tokens")
+    L = 16384
+    q, k, v = _qkv(1, 1, L, L, torch.float16, seed=41)
+    out = _run(q, k, v, scale=D ** -0.5)
+    assert torch.equal(out, _run_rows32(q, k, v, scale=D ** -0.5))
+    rows = sample_rows(1, 1, L, 32, seed=42)
+    assert_parity(gather_rows(out, rows, 1, L), orc.fa_f64(q, k, v, scale=D ** -0.5, rows=rows), "d512 16384")
