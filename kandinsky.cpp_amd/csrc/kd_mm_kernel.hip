@@ -182,15 +182,17 @@ void mm_bf16(MmArgs a) {
     }
     const char *const wtile = a.w + (int64_t)n0 * a.w_nb1;
     const char *const xtile = a.x + (int64_t)m0 * a.x_nb1;
-    auto issue = [&](int kt, int st) __attribute__((always_inline)) {
+    // DMA j (of kPer) of stage kt into LDS stage buffer st: W rounds first
+    auto dma_j = [&](int kt, int st, int j) __attribute__((always_inline)) {
         lds_t *sw = sbase + st * kStage;
-        lds_t *sx = sw + kMmWTile;
-        const char *wb = wtile + kt * 64;
-        const char *xb = xtile + kt * kXRow;
+        if (j < kWRounds)
+            dma16(wtile + kt * 64, w_off[j], sw + (wave + kMmWaves * j) * 1024);
+        else
+            dma16(xtile + kt * kXRow, x_off[j - kWRounds], sw + kMmWTile + (wave + kMmWaves * (j - kWRounds)) * 1024);
+    };
+    auto issue = [&](int kt, int st) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < kWRounds; ++j) dma16(wb, w_off[j], sw + (wave + kMmWaves * j) * 1024);
-#pragma unroll
-        for (int j = 0; j < kXRounds; ++j) dma16(xb, x_off[j], sx + (wave + kMmWaves * j) * 1024);
+        for (int j = 0; j < kPer; ++j) dma_j(kt, st, j);
     };
 
     // fragment read offsets within a stage (the row part of the swizzle is
@@ -241,7 +243,11 @@ void mm_bf16(MmArgs a) {
             }
         }
     };
-    auto mfmas = [&](const vec8 fa[4], const XFrag &fb) __attribute__((always_inline)) {
+    // the 16 MFMAs of one k-step; with dma, the DMAs of stage dkt (into
+    // buffer dst) spread over them, one group after every two MFMAs, so that
+    // their data does not reach the LDS in one burst that holds up the
+    // fragment reads (5-10% over issuing a stage's DMAs together)
+    auto mfmas = [&](const vec8 fa[4], const XFrag &fb, bool dma, int dkt, int dst) __attribute__((always_inline)) {
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
             vec8 b;
@@ -253,7 +259,17 @@ void mm_bf16(MmArgs a) {
                 b = fb.b[mb];
             }
 #pragma unroll
-            for (int nb = 0; nb < 4; ++nb) acc[nb][mb] = E::mfma(fa[nb], b, acc[nb][mb]);
+            for (int hp = 0; hp < 2; ++hp) {
+#pragma unroll
+                for (int nb = 2 * hp; nb < 2 * hp + 2; ++nb) acc[nb][mb] = E::mfma(fa[nb], b, acc[nb][mb]);
+                __builtin_amdgcn_sched_barrier(0);
+                if (dma) {
+#pragma unroll
+                    for (int j = 0; j < kPer; ++j)
+                        if (j * 8 / kPer == 2 * mb + hp) dma_j(dkt, dst, j);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     };
     // a stage is complete in LDS for every wave: this wave's DMAs of it have
@@ -272,10 +288,10 @@ void mm_bf16(MmArgs a) {
         __syncthreads();
     };
 
-    // Step kt (stage st = kt % S): start the DMA of stage kt+S-1; 16 MFMAs of
-    // k-step 0 while the fragments of k-step 1 load; publish stage kt+1 (its
-    // DMAs landed, later stages' may be in flight); 16 MFMAs of k-step 1
-    // while the fragments of stage kt+1's k-step 0 load.
+    // Step kt (stage st = kt % S): 16 MFMAs of k-step 0 while the fragments
+    // of k-step 1 load, the DMAs of stage kt+S-1 spread over them; publish
+    // stage kt+1 (its DMAs landed, later stages' may be in flight); 16 MFMAs
+    // of k-step 1 while the fragments of stage kt+1's k-step 0 load.
     constexpr int kLead = kS - 1;
     const int nk = a.K / kMmBK;
 #pragma unroll
@@ -291,22 +307,21 @@ void mm_bf16(MmArgs a) {
         const int st1 = st == kS - 1 ? 0 : st + 1;
         // stage kt+S-1 goes into the buffer of stage kt-1, whose reads all
         // completed before the previous barrier (its fence drains them)
-        if (kt + kLead < nk) issue(kt + kLead, st == 0 ? kS - 1 : st - 1);
         read(st, 1, fa1, fb1);
         __builtin_amdgcn_sched_barrier(0);
-        mfmas(fa0, fb0);
+        mfmas(fa0, fb0, kt + kLead < nk, kt + kLead, st == 0 ? kS - 1 : st - 1);
         __builtin_amdgcn_sched_barrier(0);
         publish(min(kLead, nk - 1 - kt) - 1);
         read(st1, 0, fa0, fb0);
         __builtin_amdgcn_sched_barrier(0);
-        mfmas(fa1, fb1);
+        mfmas(fa1, fb1, false, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
         st = st1;
     }
     read(st, 1, fa1, fb1);
     __builtin_amdgcn_sched_barrier(0);
-    mfmas(fa0, fb0);
-    mfmas(fa1, fb1);
+    mfmas(fa0, fb0, false, 0, 0);
+    mfmas(fa1, fb1, false, 0, 0);
     static_assert(kPer == (XF32 ? 12 : 8), "per-stage DMA count");
 
     // ---- epilogue: dst[m][n .. n+3] = acc (+ bias) ----------------------------
