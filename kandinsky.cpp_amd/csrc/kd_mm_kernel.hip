@@ -121,11 +121,14 @@ hipError_t launch_dequant(const DqArgs &a, hipStream_t s) {
 //   X stage: 256 rows x 128 bytes (F32) or 64 bytes (BF16); chunk c of row
 //            r at c ^ ((r >> 1) & 7) (F32) or c ^ ((r >> 2) & 3) (BF16)
 // -- so that the 16 rows one 16-lane group of an operand read touches fill
-// the 256 bytes of the 64 banks exactly once.  F32 X is rounded to BF16 as its fragments are read.  Per stage a
-// wave reads 8 W and 8 X fragments and issues 32 MFMAs; the only barrier is
-// the one that publishes a stage.  Rows past M or N read clamped (repeated)
-// rows and are not stored; the workgroups of one row of tiles (all n tiles
-// of 256 tokens) run on one XCD, so its L2 serves their shared X stages.
+// the 256 bytes of the 64 banks exactly once.  F32 X is rounded to BF16
+// next to the MFMAs that use its fragments.  Per stage a wave reads 8 W and
+// 8 X fragments and issues 32 MFMAs, with the DMAs of a later stage spread
+// over the first 16; the only barrier is the one that publishes a stage.
+// Rows past M or N read clamped (repeated) rows and are not stored; the
+// workgroups of one row of tiles (all n tiles of 256 tokens) run on one XCD,
+// so its L2 serves their shared X stages.  The output goes through LDS so
+// that its stores are whole 128-byte lines.
 // ---------------------------------------------------------------------------
 constexpr int kMmWaves = 4;
 constexpr int kMmWTile = kMmBN * kMmBK * 2;   // 16 KiB
