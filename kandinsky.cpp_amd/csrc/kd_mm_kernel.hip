@@ -333,7 +333,8 @@ void mm_bf16(MmArgs a) {
     // wave's own 16 KiB (chunk index XOR (row >> 1) & 7: no bank conflicts),
     // then lane L reads chunk L % 8 of row 8j + L / 8, so that every store
     // instruction writes eight whole 128-byte lines of dst instead of
-    // 32-byte pieces of 32 rows.  The stage buffers are free once every wave
+    // 32-byte pieces of 32 rows, as streaming (nontemporal) stores: dst is
+    // not read again here (1%).  The stage buffers are free once every wave
     // is past its last read; after that a wave touches only its own region
     // (its LDS operations complete in order).
     __syncthreads();
@@ -365,7 +366,7 @@ void mm_bf16(MmArgs a) {
             const int m = m0 + 128 * wm + row;
             if (m < a.M && n < a.N) {
                 v.x += bias.x; v.y += bias.y; v.z += bias.z; v.w += bias.w;
-                *reinterpret_cast<f32x4 *>(a.dst + (int64_t)m * a.d_nb1 + (int64_t)n * 4) = v;
+                __builtin_nontemporal_store(v, reinterpret_cast<f32x4 *>(a.dst + (int64_t)m * a.d_nb1 + (int64_t)n * 4));
             }
         }
     }
