@@ -10,8 +10,9 @@
   and against the oracle's restatement of ggml's CPU path (x rounded to
   Q8_0): reported and bounded (cosine >= 0.9999).
 The shapes walk the 256 x 256 tiles and 32-k stages: M and N below, at and
-past a tile, K of one to many stages, x as F32 and BF16, 3-D x, bias on and
-off, and the 31,744-token DiT projection shape with sampled rows.
+past a tile, K of one to many stages, both tile orders (output tiles a
+multiple of 4 or not), x as F32 and BF16, 3-D x, bias on and off, and the
+31,744-token DiT projection shape with sampled rows.
 """
 import numpy as np
 import pytest
@@ -72,6 +73,10 @@ CASES = [
     (257, 1024, 512, "q4_0", torch.bfloat16, False),
     (64, 128, 160, "f16", torch.bfloat16, True),
     (100, 36, 1024, "f32", torch.float32, True),
+    # output tiles a multiple of 4 (the column-grouped tile order) with
+    # partial last tiles in both directions
+    (600, 2000, 128, "bf16", torch.bfloat16, True),
+    (70, 1000, 224, "q8_0", torch.float32, False),
 ]
 
 
