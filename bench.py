@@ -43,6 +43,9 @@ def parse():
     p.add_argument("--cpu-rows", type=int, default=2048, help="query rows per (b, h) in the CPU sample")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only copy 1 GiB device-to-device 3 times (scales the PMC byte counters)")
+    p.add_argument("--linear-only", action="store_true",
+                   help="time only the 63,488 x 4096 x 4096 projection (BF16 weight rows, F32 x, bias) "
+                        "and print its ms per call (for counter runs)")
     p.add_argument("--cross-only", action="store_true",
                    help="only the text cross-attention (C2 shape): for counter runs of its kernel")
     return p.parse_args()
@@ -139,6 +142,20 @@ def main():
         dx = kd_fa.make_desc(qx, kx, vx, mx, ox, 1.0 / D ** 0.5)
         msx = time_launches(torch, lambda: kd_fa.run_desc(dx, None, stream), args.steps, args.warmup, stream)
         print(json.dumps({"cross_attn_ms": round(msx, 4)}))
+        return
+    if args.linear_only:
+        import kd_mm
+        Mx = B * L
+        xl = rand(torch, (Mx, 4096), 51, dev, torch.float32)
+        yl = torch.empty((Mx, 4096), device=dev, dtype=torch.float32)
+        bl = rand(torch, (4096,), 52, dev, torch.float32)
+        wl = rand(torch, (4096, 4096), 53, dev, bf) * 0.05
+        dl = kd_mm.make_desc(wl, xl, bl, yl)
+        st = kd_mm.run_desc(dl, None, stream)
+        if st != 0:
+            raise kd_fa.KdFaError(st, "kd_mm_run")
+        msl = time_launches(torch, lambda: kd_mm.run_desc(dl, None, stream), args.steps, args.warmup, stream)
+        print(json.dumps({"linear_ms": round(msl, 4), "tflops": round(2.0 * Mx * 4096 * 4096 / (msl * 1e-3) / 1e12, 2)}))
         return
     q = rand(torch, (B, HEADS, L, D), 3, dev, bf)
     k = rand(torch, (B, HEADS, L, D), 1003, dev, bf)
