@@ -76,6 +76,10 @@ CASES = [
     (1, 4, 4, 1, 31, 200, torch.float16, torch.float16, "pad"),
     (2, 8, 8, 2, 4096, 200, torch.bfloat16, torch.float32, None),
     (2, 8, 8, 2, 4096, 256, torch.float16, torch.float32, "pad"),
+    # the largest key set with a partial last chunk (no mask: this kernel),
+    # and a masked one whose mask rows stop at Lk (the 32-row kernel)
+    (1, 2, 2, 1, 70, 255, torch.bfloat16, torch.float32, None),
+    (1, 2, 2, 1, 64, 129, torch.float16, torch.bfloat16, "rand"),
 ]
 
 
