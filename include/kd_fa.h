@@ -69,7 +69,7 @@ enum {
     KD_FA_ERR_TYPE       = -2,   /* unsupported tensor type               */
     KD_FA_ERR_SHAPE      = -3,   /* shapes inconsistent with the op       */
     KD_FA_ERR_LAYOUT     = -4,   /* stride / alignment not supported      */
-    KD_FA_ERR_PARAM      = -5,   /* max_bias, softcap or scale unsupported */
+    KD_FA_ERR_PARAM      = -5,   /* max_bias, softcap, sinks or scale unsupported */
     KD_FA_ERR_ROPE       = -6,   /* invalid RoPE or norm descriptor       */
     KD_FA_ERR_LAUNCH     = -7,   /* HIP launch failed                     */
     KD_FA_ERR_DEVICE     = -8    /* no gfx950 device / runtime error      */
@@ -84,16 +84,21 @@ typedef struct kd_fa_tensor {
 } kd_fa_tensor;
 
 /*
- * The GGML_OP_FLASH_ATTN_EXT node: src[0..3] = q, k, v, mask and the op
- * params {scale, max_bias, logit_softcap, prec}
+ * The GGML_OP_FLASH_ATTN_EXT node: src[0..4] = q, k, v, mask, sinks and the
+ * op params {scale, max_bias, logit_softcap, prec}
  * (ggml_flash_attn_ext + ggml_flash_attn_ext_set_prec, ops.hpp:176-177).
  * mask.data == NULL means "no mask" (ops.hpp:171-174 passes nullptr).
+ * sinks is newer ggml's src[4] (per-head F32 logits added to each row's
+ * softmax denominator); ops.hpp:176 never sets it, and a node that carries
+ * one (sinks.data != NULL) is refused with KD_FA_ERR_PARAM so that the
+ * caller keeps its fallback.  Zero-initialise it.
  */
 typedef struct kd_fa_desc {
     kd_fa_tensor q;
     kd_fa_tensor k;
     kd_fa_tensor v;
     kd_fa_tensor mask;
+    kd_fa_tensor sinks;
     kd_fa_tensor dst;
     float   scale;
     float   max_bias;
@@ -201,10 +206,12 @@ typedef struct kd_fa_qk_norm {
  * every step in F32 as kd_fa_qk_norm and kd_fa_rope_run state.
  * workspace != NULL: K is transformed once into it (as kd_fa_rope_run_ws,
  * same size rule; it holds k' afterwards); NULL: K tiles are transformed
- * on load.  The two give bitwise equal results.  With a workspace K may be
- * F32 -- the projection output, normalised and rotated before the one
- * rounding to V's type, the reference's order (ops.hpp:167 casts after
- * RoPE); kd_fa_dit_supports accepts an F32 K on that condition.
+ * on load.  The two give bitwise equal results.  K may be F32 -- the
+ * projection output, normalised and rotated before the one rounding to V's
+ * type, the reference's order (ops.hpp:167 casts after RoPE) -- when K is
+ * transformed (a K norm weight or a RoPE mode); the workspace is then
+ * mandatory (KD_FA_ERR_NULL without one).  kd_fa_dit_supports accepts an
+ * F32 K on exactly that condition.
  * norm == NULL and rope == NULL is kd_fa_run.
  */
 int kd_fa_dit_run(const kd_fa_desc *desc, const kd_fa_rope *rope, const kd_fa_qk_norm *norm,
@@ -250,6 +257,24 @@ int kd_fa_rope_axes_fill(int T, int Hp, int Wp, const int axes[3],
  * with: out[pos][D] interleaved (cos, sin) of pos * freq_i.
  */
 int kd_fa_rope_text_table(int L, int D, float theta, float *out);
+
+/*
+ * kd_fa_set_routing - comparison hook for tests and tuning; it has no
+ * counterpart in the reference.  Without it the kernel that runs a node is
+ * a function of the node alone.  The specialised kernels compute every row
+ * with the same arithmetic as the general 32-row kernel (bitwise equal
+ * results), and these flags take them out of the choice so that a test can
+ * compare the two.  Process-wide (an atomic read once per call); returns
+ * the previous flags.  Production callers never call it.
+ */
+enum {
+    KD_FA_ROUTE_DEFAULT = 0,
+    KD_FA_ROUTE_NO_W64  = 1,   /* unmasked calls: the 32-row kernel, not the 64-row one   */
+    KD_FA_ROUTE_NO_XRES = 2,   /* short key sets: the 32-row kernel, not the LDS-resident */
+    KD_FA_ROUTE_D512_R1 = 4,   /* D = 512: one 32-row block per workgroup                 */
+    KD_FA_ROUTE_NO_SPLIT = 8   /* short query sets: no key split (one pass per row)      */
+};
+int kd_fa_set_routing(int flags);
 
 /* Human-readable text for a KD_FA_* status code. */
 const char *kd_fa_strerror(int status);

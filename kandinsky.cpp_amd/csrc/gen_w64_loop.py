@@ -10,7 +10,8 @@ another tile of the same wave.  Per 64-key tile t (step t):
 
   phase 1   MFMA  S(t+1) = K(t+1) Q^T       32 x 32x32x16, K fragments from LDS
             VALU  softmax of S(t), keys 32-63   (exp2, round to T, row sums)
-  check     a row whose weight sum left [0, 2^64]: exact max, rescale, redo
+  check     a row whose weight sum left [0, cap]: exact max, rescale, redo
+            (cap 2^64 for BF16, 2^15 for F16: every rounded weight stays finite)
   phase 2   MFMA  O^T += V(t)^T P(t)^T       32 x 32x32x16, V^T by ds_read_b64_tr_b16
             VALU  softmax of S(t+1), keys 0-31
 
@@ -30,8 +31,12 @@ instruction there: without them the reader sees the value from before the
 dot2), M0 and the LDS DMA that reads it; and an lgkmcnt wait before the
 first use of every LDS load (at most 15 in flight).
 
-Usage: python3 gen_w64_loop.py [out]  (default: kd_fa_w64_loop.inc beside it)
+Usage: python3 gen_w64_loop.py [out] [--kpre N] [--vpre N] [--per1 N] [--check-at N]
+(default out: kd_fa_w64_loop.inc beside it).  The schedule knobs are
+tuning switches for variant builds; the committed loop uses the defaults,
+and the environment is never read.
 """
+import argparse
 import os
 import re
 
@@ -54,13 +59,10 @@ V_LAST = 247
 A_O = 0                # O[qb][dblk] -> +64*qb + 16*dblk, 16 floats
 A_Q = 128              # Q[qb][ks] -> +32*qb + 4*ks
 # LDS operand prefetch distances: K fragments KPRE k-steps ahead, V^T
-# fragments VPRE fragments ahead (ring slots: KPRE + 1 and VPRE + 2)
-KPRE = int(os.environ.get("KD_W64_KPRE", "2"))
-VPRE = int(os.environ.get("KD_W64_VPRE", "2"))
+# fragments VPRE fragments ahead (ring slots: KPRE + 1 and VPRE + 2); set by
+# configure() from the command line
+KPRE = VPRE = A_VF = A_LAST = None
 A_KF = 192             # K fragments: (KPRE + 1) slots x 2 key blocks x 4
-A_VF = A_KF + 8 * (KPRE + 1)   # V^T fragments: (VPRE + 2) slots x 4
-A_LAST = A_VF + 4 * (VPRE + 2) - 1
-assert A_LAST <= 255
 # SGPRs s84..s95
 S_K = 84               # s[84:87] K buffer resource (moves one tile per DMA)
 S_V = 88               # s[88:91] V buffer resource
@@ -76,8 +78,23 @@ Q_OFF = 65536
 
 # Phase 1 schedule: VALU instructions after each MFMA, and the MFMA after
 # which the row check runs (the rest of S(t+1) is computed meanwhile)
-PER1 = int(os.environ.get("KD_W64_PER1", "4"))
-CHECK_AT = int(os.environ.get("KD_W64_CHECK_AT", "30"))
+PER1 = CHECK_AT = None
+
+# Row-sum cap of the lazy running max, as an F32 bit pattern: the weights are
+# rounded to the operand type for PV, so the cap stays inside its range
+SUM_CAP = {"bf16": "0x5f800000",   # 2^64
+           "f16": "0x47000000"}    # 2^15 (F16's largest finite value is 65504)
+
+
+def configure(kpre=2, vpre=2, per1=4, check_at=30):
+    global KPRE, VPRE, A_VF, A_LAST, PER1, CHECK_AT
+    KPRE, VPRE, PER1, CHECK_AT = kpre, vpre, per1, check_at
+    A_VF = A_KF + 8 * (KPRE + 1)   # V^T fragments: (VPRE + 2) slots x 4
+    A_LAST = A_VF + 4 * (VPRE + 2) - 1
+    assert A_LAST <= 255
+
+
+configure()
 
 MFMA_WS = 20           # MFMA result -> VALU / LDS / accvgpr access
 VALU_MFMA_WS = 4       # VALU or accvgpr write -> MFMA operand read
@@ -382,7 +399,7 @@ class Gen:
         tr.emit(valu(f"v_mov_b32 {vr(Y)}, {vr(s1)}", {vr(s1)}, {vr(Y)}))
         tr.emit(Ins(f"v_permlane32_swap_b32 {vr(X)}, {vr(Y)}", "perm", {vr(X), vr(Y)}, {vr(X), vr(Y)}))
         tr.emit(valu(f"v_add_f32 {vr(X)}, {vr(X)}, {vr(Y)}", {vr(X), vr(Y)}, {vr(X)}))
-        tr.emit(valu(f"v_cmp_nge_f32 vcc, 0x5f800000, {vr(X)}", {vr(X)}, ()))
+        tr.emit(valu(f"v_cmp_nge_f32 vcc, {SUM_CAP[self.T]}, {vr(X)}", {vr(X)}, ()))
         tr.emit(Ins(f"s_cbranch_vccnz {slow}", "branch"))
         tr.label(back)
         for qb in range(2):
@@ -580,7 +597,8 @@ def check_registers(lines):
             assert S_FIRST <= int(m.group(1)) <= S_LAST + 3, ln
 
 
-def main(path=None):
+def main(path=None, kpre=2, vpre=2, per1=4, check_at=30):
+    configure(kpre, vpre, per1, check_at)
     here = os.path.dirname(os.path.abspath(__file__))
     path = path or os.path.join(here, "kd_fa_w64_loop.inc")
     out = ["// Generated by gen_w64_loop.py from this directory; do not edit.",
@@ -604,5 +622,11 @@ def main(path=None):
 
 
 if __name__ == "__main__":
-    import sys
-    main(sys.argv[1] if len(sys.argv) > 1 else None)
+    ap = argparse.ArgumentParser(description="write the fa_fwd_w64 key loop")
+    ap.add_argument("out", nargs="?", default=None)
+    ap.add_argument("--kpre", type=int, default=2)
+    ap.add_argument("--vpre", type=int, default=2)
+    ap.add_argument("--per1", type=int, default=4)
+    ap.add_argument("--check-at", type=int, default=30)
+    args = ap.parse_args()
+    main(args.out, args.kpre, args.vpre, args.per1, args.check_at)

@@ -37,10 +37,12 @@ constexpr float kLog2e = 1.4426950408889634f;
 // Lazy rescale: the running max moves only when a row max exceeds it by
 // more than kTau (log2 units), so P <= 2^kTau before normalisation.
 constexpr float kTau = 8.0f;
-// Unmasked path: a row's weights against the running max may grow up to
-// this sum before the max is refreshed (2^64: no F32 overflow of O for any
-// |V| < 2^40 and Lk < 2^20).
-constexpr float kSumCap = 18446744073709551616.0f;
+// Unmasked path: a row's weights of one 64-key tile, taken against the
+// running max, may sum up to Elem<T>::kSumCap before the max is refreshed.
+// Every weight is at most that sum and is rounded to T for the PV product,
+// so the cap must stay inside T's finite range: BF16 2^64 (no F32 overflow
+// of O for any |V| < 2^40 and Lk < 2^20); F16 2^15, below its largest
+// finite value 65504 -- a weight of 2^16 would round to +inf.
 
 // ---------------------------------------------------------------------
 // element-type traits: MFMA and F32 <-> storage conversions
@@ -49,6 +51,7 @@ template <typename T> struct Elem;
 
 template <> struct Elem<__bf16> {
     typedef bf16x8 vec8;
+    static constexpr float kSumCap = 18446744073709551616.0f;   // 2^64
     static __device__ __forceinline__ f32x16 mfma(vec8 a, vec8 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
     }
@@ -62,6 +65,7 @@ template <> struct Elem<__bf16> {
 
 template <> struct Elem<_Float16> {
     typedef f16x8 vec8;
+    static constexpr float kSumCap = 32768.0f;                  // 2^15
     static __device__ __forceinline__ f32x16 mfma(vec8 a, vec8 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
     }

@@ -7,7 +7,6 @@
 #include <algorithm>
 #include <atomic>
 #include <cmath>
-#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -30,8 +29,9 @@ bool is_16b(const void *p) { return is_16b(reinterpret_cast<uintptr_t>(p)); }
 // Conditions of kd_fa_supports (and of the RoPE and norm descriptors when
 // given).  `mask_vec` reports whether the mask rows can be read 16 bytes at
 // a time.
-// k_f32: an F32 K is accepted (kd_fa_dit_run with a workspace, where the K
-// pre-pass rounds it to V's type).
+// k_f32: an F32 K is accepted (K is transformed, by a norm weight or RoPE;
+// run() then also requires the workspace, whose pre-pass rounds K to V's
+// type).
 int validate(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, bool *mask_vec,
              bool k_f32 = false) {
     if (!d) return KD_FA_ERR_NULL;
@@ -46,8 +46,10 @@ int validate(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, b
     if (o.type != KD_FA_TYPE_F32 && o.type != KD_FA_TYPE_F16 && o.type != KD_FA_TYPE_BF16) return KD_FA_ERR_TYPE;
     if (m.data && m.type != KD_FA_TYPE_F16) return KD_FA_ERR_TYPE;
 
-    // op params: plain softmax attention only (ops.hpp:176 passes 0, 0)
+    // op params: plain softmax attention only (ops.hpp:176 passes 0, 0 and
+    // no sinks)
     if (d->max_bias != 0.0f || d->logit_softcap != 0.0f) return KD_FA_ERR_PARAM;
+    if (d->sinks.data) return KD_FA_ERR_PARAM;
     if (!std::isfinite(d->scale)) return KD_FA_ERR_PARAM;
 
     // shapes
@@ -127,6 +129,9 @@ int validate(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, b
 // gfx950 check, once per device.
 std::atomic<int> g_dev_state[64];
 
+// KD_FA_ROUTE_* flags of kd_fa_set_routing (tests and tuning only).
+std::atomic<int> g_route{KD_FA_ROUTE_DEFAULT};
+
 int device_ok() {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return KD_FA_ERR_DEVICE;
@@ -156,11 +161,10 @@ size_t rope_ws_bytes(const kd_fa_desc *d) {
 
 // The 64-rows-per-wave kernel takes the unmasked calls whose K streams from
 // memory as stored (no transform on load) and whose keys fill whole 64-key
-// tiles; its buffer-resource offsets are 32-bit.  KD_FA_W64=0 in the
-// environment routes every call to the 32-row kernel (for comparisons).
-static bool use_w64(const kdfa::Args &a, bool k_on_load) {
-    const char *e = std::getenv("KD_FA_W64");
-    if ((e && e[0] == '0') || a.m || k_on_load || a.Lk < 64 || a.Lk % 64 != 0) return false;
+// tiles; its buffer-resource offsets are 32-bit.  KD_FA_ROUTE_NO_W64 routes
+// every call to the 32-row kernel (for comparisons).
+static bool use_w64(const kdfa::Args &a, bool k_on_load, int route) {
+    if ((route & KD_FA_ROUTE_NO_W64) || a.m || k_on_load || a.Lk < 64 || a.Lk % 64 != 0) return false;
     const int64_t lim = (int64_t)1 << 31;
     return (int64_t)(a.Lk - 1) * a.k_nb1 + 256 < lim && (int64_t)(a.Lk - 1) * a.v_nb1 + 256 < lim;
 }
@@ -168,11 +172,10 @@ static bool use_w64(const kdfa::Args &a, bool k_on_load) {
 // Short key sets (the text cross-attention) go to the kernel that keeps K
 // and V in LDS, when K is read as stored, Q is not rotated and stored as F32
 // or in K's type, and a mask's rows are 16-byte aligned and hold every
-// 8-key chunk that starts below Lk.  KD_FA_XRES=0 in the environment routes
-// them to the 32-row kernel (for comparisons).
-static bool use_xres(const kdfa::Args &a, const kd_fa_desc *d, bool k_on_load) {
-    const char *e = std::getenv("KD_FA_XRES");
-    if ((e && e[0] == '0') || k_on_load || a.rope_mode != KD_FA_ROPE_NONE) return false;
+// 8-key chunk that starts below Lk.  KD_FA_ROUTE_NO_XRES routes them to the
+// 32-row kernel (for comparisons).
+static bool use_xres(const kdfa::Args &a, const kd_fa_desc *d, bool k_on_load, int route) {
+    if ((route & KD_FA_ROUTE_NO_XRES) || k_on_load || a.rope_mode != KD_FA_ROPE_NONE) return false;
     if (a.Lk > kdfa::kXresMaxKeys) return false;
     if (a.q_type != KD_FA_TYPE_F32 && a.q_type != d->v.type) return false;
     if (a.m && (!a.mask_vec || d->mask.ne[0] < ((int64_t)a.Lk + 7) / 8 * 8)) return false;
@@ -198,11 +201,14 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
     bool mask_vec = false;
     const bool rope_on = r && r->mode != KD_FA_ROPE_NONE;
     const bool k_xform = rope_on || (n && n->k_weight);
-    int st = validate(d, r, n, &mask_vec, ws && k_xform);
+    int st = validate(d, r, n, &mask_vec, k_xform);
     if (st != KD_FA_OK) return st;
+    // an F32 K is rounded to V's type by the workspace pre-pass only
+    if (!ws && k_xform && d->k.type == KD_FA_TYPE_F32) return KD_FA_ERR_NULL;
     if (ws && k_xform) {
         if (!is_16b(ws) || ws_bytes < rope_ws_bytes(d)) return KD_FA_ERR_LAYOUT;
     }
+    const int route = g_route.load(std::memory_order_relaxed);
     const int64_t Lq = d->q.ne[1], H = d->q.ne[2], B = d->q.ne[3];
     if (Lq == 0 || H == 0 || B == 0) return KD_FA_OK;
     st = device_ok();
@@ -253,10 +259,9 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
     hipStream_t hs = static_cast<hipStream_t>(stream);
     if (d->q.ne[0] == kHeadDimVae) {
         // 64 query rows per workgroup (half the key stream per row) when that
-        // still gives every CU a workgroup, else 32; KD_FA_D512_ROWS=32 in the
-        // environment forces 32 (for comparisons)
-        const char *e = std::getenv("KD_FA_D512_ROWS");
-        const int rows = ((e && std::atoi(e) == 32) || (Lq + 63) / 64 * H * B < 256) ? 32 : 64;
+        // still gives every CU a workgroup, else 32; KD_FA_ROUTE_D512_R1
+        // forces 32 (for comparisons)
+        const int rows = ((route & KD_FA_ROUTE_D512_R1) || (Lq + 63) / 64 * H * B < 256) ? 32 : 64;
         a.n_qt = (int32_t)((Lq + rows - 1) / rows);
         a.n_blocks = (int32_t)(a.n_qt * H * B);
         return kdfa::launch_d512(a, d->v.type, rows, hs) == hipSuccess ? KD_FA_OK : KD_FA_ERR_LAUNCH;
@@ -280,11 +285,12 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
         a.k_nb3 = row * a.Lk * hk;
     }
     hipError_t e;
-    if (use_xres(a, d, k_rope)) {
+    if (use_xres(a, d, k_rope, route)) {
         xres_split(a);
         e = kdfa::launch_xres(a, d->v.type, hs);
     } else {
-        e = use_w64(a, k_rope) ? kdfa::launch_w64(a, d->v.type, hs) : kdfa::launch(a, d->v.type, k_rope, hs);
+        e = use_w64(a, k_rope, route) ? kdfa::launch_w64(a, d->v.type, hs)
+                                      : kdfa::launch(a, d->v.type, k_rope, hs);
     }
     if (e != hipSuccess) return KD_FA_ERR_LAUNCH;
     return KD_FA_OK;
@@ -330,7 +336,9 @@ int kd_fa_rope_run(const kd_fa_desc *desc, const kd_fa_rope *rope, void *stream)
 
 int kd_fa_dit_supports(const kd_fa_desc *desc, const kd_fa_rope *rope, const kd_fa_qk_norm *norm,
                        int *reason) {
-    const int st = validate(desc, rope, norm, nullptr, true);
+    // an F32 K only when K is transformed (then through the workspace)
+    const bool k_xform = (rope && rope->mode != KD_FA_ROPE_NONE) || (norm && norm->k_weight);
+    const int st = validate(desc, rope, norm, nullptr, k_xform);
     if (reason) *reason = st;
     return st == KD_FA_OK ? 1 : 0;
 }
@@ -428,7 +436,7 @@ const char *kd_fa_strerror(int status) {
     case KD_FA_ERR_TYPE: return "unsupported tensor type";
     case KD_FA_ERR_SHAPE: return "tensor shapes inconsistent with GGML_OP_FLASH_ATTN_EXT";
     case KD_FA_ERR_LAYOUT: return "unsupported stride or alignment";
-    case KD_FA_ERR_PARAM: return "unsupported op parameter (max_bias, logit_softcap, scale)";
+    case KD_FA_ERR_PARAM: return "unsupported op parameter (max_bias, logit_softcap, sinks, scale)";
     case KD_FA_ERR_ROPE: return "invalid RoPE descriptor";
     case KD_FA_ERR_LAUNCH: return "HIP kernel launch failed";
     case KD_FA_ERR_DEVICE: return "current device is not a gfx950 GPU";
@@ -436,6 +444,8 @@ const char *kd_fa_strerror(int status) {
     }
 }
 
-int kd_fa_version(void) { return 100; }
+int kd_fa_version(void) { return 200; }
+
+int kd_fa_set_routing(int flags) { return g_route.exchange(flags); }
 
 }  // extern "C"

@@ -479,10 +479,10 @@ void fa_fwd_d128(Args a) {
     // key0+63) and O^T += V^T P^T with the V rows at vs_.  The running max
     // m_run is not refreshed every step: the exponents are taken against the
     // current m_run, and only when a row's sum of weights leaves
-    // [0, 2^kSumCap] (a score far above m_run, or the first step with
+    // [0, E::kSumCap] (a score far above m_run, or the first step with
     // m_run = -inf) is the step's exact row max computed, O rescaled and the
-    // exponents redone.  Weights stay <= 2^kSumCap, far inside the F32 /
-    // bf16 range.  TAIL: keys past Lk (last tile only) read clamped K rows,
+    // exponents redone.  Weights stay <= E::kSumCap, inside T's finite range
+    // once rounded for the PV product.  TAIL: keys past Lk (last tile only) read clamped K rows,
     // i.e. copies of key Lk-1 -- finite scores that never raise the row
     // max; their weights are zeroed after the exponent.
     auto soft_pv = [&](auto tail_c, int key0, const f32x16 &s0, const f32x16 &s1, const lds_t *vs_) __attribute__((always_inline)) {
@@ -508,7 +508,7 @@ void fa_fwd_d128(Args a) {
         float sum = pack_sum(p, pb);
         const float pair = pair_sum(sum);
         // !(x <= cap) also catches NaN (inf - inf with m_run = -inf)
-        if (__builtin_amdgcn_ballot_w64(!(pair <= kSumCap)) != 0) {
+        if (__builtin_amdgcn_ballot_w64(!(pair <= E::kSumCap)) != 0) {
             float q[32];
 #pragma unroll
             for (int i = 0; i < 16; ++i) { q[i] = s0[i]; q[16 + i] = s1[i]; }
@@ -596,8 +596,8 @@ void fa_fwd_d128(Args a) {
             float sum = pack_sum(p, pb);
             if (NEXT) sched_pipe<kKPre, KD_FA_PIPE_VPM>();
             const float pair = pair_sum(sum);
-            // the weight sum left [0, 2^kSumCap]: exact max, rescale, redo
-            if (__builtin_amdgcn_ballot_w64(!(pair <= kSumCap)) != 0) {
+            // the weight sum left [0, E::kSumCap]: exact max, rescale, redo
+            if (__builtin_amdgcn_ballot_w64(!(pair <= E::kSumCap)) != 0) {
                 float q[32];
 #pragma unroll
                 for (int i = 0; i < 16; ++i) { q[i] = c0[i]; q[16 + i] = c1[i]; }
@@ -1029,7 +1029,7 @@ void fa_fwd_xres(Args a) {
         pv(sV + t * kTileBytes, pb);
     };
     // unmasked tile: weights against the current running max, the exact max
-    // and a redo only when a row's weight sum leaves [0, kSumCap]; keys past
+    // and a redo only when a row's weight sum leaves [0, E::kSumCap]; keys past
     // Lk (repeats of key Lk - 1) get weight 0
     auto tile_plain = [&](auto part_c, int t) __attribute__((always_inline)) {
         constexpr bool tail = decltype(part_c)::value;
@@ -1056,7 +1056,7 @@ void fa_fwd_xres(Args a) {
         drop_tail(p);
         float sum = pack_sum(p, pb);
         const float pair = pair_sum(sum);
-        if (__builtin_amdgcn_ballot_w64(!(pair <= kSumCap)) != 0) {
+        if (__builtin_amdgcn_ballot_w64(!(pair <= E::kSumCap)) != 0) {
             float q[32];
 #pragma unroll
             for (int i = 0; i < 16; ++i) { q[i] = s0[i]; q[16 + i] = s1[i]; }

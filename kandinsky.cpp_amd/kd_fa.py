@@ -50,6 +50,13 @@ ERR_ROPE = -6
 ERR_LAUNCH = -7
 ERR_DEVICE = -8
 
+# kd_fa_set_routing flags (comparison hooks for tests and tuning)
+ROUTE_DEFAULT = 0
+ROUTE_NO_W64 = 1
+ROUTE_NO_XRES = 2
+ROUTE_D512_R1 = 4
+ROUTE_NO_SPLIT = 8
+
 
 class KdFaTensor(ctypes.Structure):
     """struct kd_fa_tensor: a ggml tensor view (type, ne, nb, data)."""
@@ -70,6 +77,7 @@ class KdFaDesc(ctypes.Structure):
         ("k", KdFaTensor),
         ("v", KdFaTensor),
         ("mask", KdFaTensor),
+        ("sinks", KdFaTensor),
         ("dst", KdFaTensor),
         ("scale", ctypes.c_float),
         ("max_bias", ctypes.c_float),
@@ -150,6 +158,8 @@ def _lib():
         lib.kd_fa_strerror.restype = ctypes.c_char_p
         lib.kd_fa_version.argtypes = []
         lib.kd_fa_version.restype = ctypes.c_int
+        lib.kd_fa_set_routing.argtypes = [ctypes.c_int]
+        lib.kd_fa_set_routing.restype = ctypes.c_int
         _LIB = lib
     return _LIB
 
@@ -157,6 +167,24 @@ def _lib():
 def lib():
     """The loaded libkd_fa.so (raises if it is not built)."""
     return _lib()
+
+
+class routing:
+    """Context manager over kd_fa_set_routing: ``with routing(ROUTE_NO_W64):``
+    runs the enclosed calls with the flagged kernels taken out of the choice
+    (a comparison hook for tests; production calls never set it)."""
+
+    def __init__(self, flags: int):
+        self.flags = int(flags)
+        self.prev = None
+
+    def __enter__(self):
+        self.prev = _lib().kd_fa_set_routing(self.flags)
+        return self
+
+    def __exit__(self, *exc):
+        _lib().kd_fa_set_routing(self.prev)
+        return False
 
 
 def header_symbols(path: str = HEADER_PATH) -> list[str]:

@@ -261,6 +261,9 @@ static int check_desc(const kd_fa_desc *d, const kd_fa_rope *r, int need_dst) {
     if (need_dst && d->dst.type != KD_FA_TYPE_F32) return KD_FA_ERR_TYPE;
     /* ALiBi (max_bias > 0) is not restated: the op is only built with 0. */
     if (d->max_bias != 0.0f) return KD_FA_ERR_PARAM;
+    /* Attention sinks (newer ggml's src[4]) are not restated either: the
+       reference never sets them (ops.hpp:176). */
+    if (d->sinks.data) return KD_FA_ERR_PARAM;
     if (d->k.ne[0] != d->q.ne[0] || d->k.ne[1] != d->v.ne[1]) return KD_FA_ERR_SHAPE;
     if (d->k.ne[2] <= 0 || d->q.ne[2] % d->k.ne[2] || d->k.ne[3] <= 0 || d->q.ne[3] % d->k.ne[3]) return KD_FA_ERR_SHAPE;
     if (d->v.ne[2] <= 0 || d->q.ne[2] % d->v.ne[2] || d->v.ne[3] <= 0 || d->q.ne[3] % d->v.ne[3]) return KD_FA_ERR_SHAPE;

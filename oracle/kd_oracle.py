@@ -30,7 +30,7 @@ class Tensor(ctypes.Structure):
 
 
 class Desc(ctypes.Structure):
-    _fields_ = [("q", Tensor), ("k", Tensor), ("v", Tensor), ("mask", Tensor), ("dst", Tensor),
+    _fields_ = [("q", Tensor), ("k", Tensor), ("v", Tensor), ("mask", Tensor), ("sinks", Tensor), ("dst", Tensor),
                 ("scale", ctypes.c_float), ("max_bias", ctypes.c_float),
                 ("logit_softcap", ctypes.c_float), ("prec", ctypes.c_int32)]
 

@@ -36,8 +36,8 @@ def test_struct_layout_matches_c():
     int main(void) {
       printf("%zu %zu %zu %zu %zu\n", sizeof(kd_fa_tensor), offsetof(kd_fa_tensor, ne),
              offsetof(kd_fa_tensor, nb), offsetof(kd_fa_tensor, data), sizeof(kd_fa_desc));
-      printf("%zu %zu %zu %zu\n", offsetof(kd_fa_desc, dst), offsetof(kd_fa_desc, scale),
-             offsetof(kd_fa_desc, prec), sizeof(kd_fa_rope));
+      printf("%zu %zu %zu %zu %zu\n", offsetof(kd_fa_desc, sinks), offsetof(kd_fa_desc, dst),
+             offsetof(kd_fa_desc, scale), offsetof(kd_fa_desc, prec), sizeof(kd_fa_rope));
       printf("%zu %zu %zu %zu\n", offsetof(kd_fa_rope, table), offsetof(kd_fa_rope, axes_data),
              offsetof(kd_fa_rope, grid), offsetof(kd_fa_rope, axes));
       printf("%zu %zu %zu\n", sizeof(kd_fa_qk_norm), offsetof(kd_fa_qk_norm, k_weight),
@@ -54,7 +54,7 @@ def test_struct_layout_matches_c():
         got = [int(x) for x in subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split()]
     T, Dd, R = kd_fa.KdFaTensor, kd_fa.KdFaDesc, kd_fa.KdFaRope
     want = [ctypes.sizeof(T), T.ne.offset, T.nb.offset, T.data.offset, ctypes.sizeof(Dd),
-            Dd.dst.offset, Dd.scale.offset, Dd.prec.offset, ctypes.sizeof(R),
+            Dd.sinks.offset, Dd.dst.offset, Dd.scale.offset, Dd.prec.offset, ctypes.sizeof(R),
             R.table.offset, R.axes_data.offset, R.grid.offset, R.axes.offset,
             ctypes.sizeof(kd_fa.KdFaQkNorm), kd_fa.KdFaQkNorm.k_weight.offset, kd_fa.KdFaQkNorm.eps.offset]
     assert got == want
@@ -134,6 +134,14 @@ def test_rejections_carry_reason():
     assert _sup(q, k, v, m, dst, max_bias=8.0) == (False, kd_fa.ERR_PARAM)
     assert _sup(q, k, v, m, dst, logit_softcap=30.0) == (False, kd_fa.ERR_PARAM)
     assert _sup(q, k, v, m, dst, scale=float("nan")) == (False, kd_fa.ERR_PARAM)
+    # attention sinks (newer ggml's src[4], never set by ops.hpp:176): refused
+    d = kd_fa.make_desc(q, k, v, m, dst, 0.1)
+    sinks = torch.zeros(4, dtype=torch.float32)
+    d.sinks = kd_fa.view(sinks)
+    reason = ctypes.c_int(0)
+    assert kd_fa.lib().kd_fa_supports(ctypes.byref(d), ctypes.byref(reason)) == 0
+    assert reason.value == kd_fa.ERR_PARAM
+    assert kd_fa.lib().kd_fa_run(ctypes.byref(d), None) == kd_fa.ERR_PARAM
     assert _sup(q, k.float(), v.float(), m, dst) == (False, kd_fa.ERR_TYPE)          # F32 K
     assert _sup(q, k, v.to(torch.bfloat16), m, dst) == (False, kd_fa.ERR_TYPE)       # V type != K type
     assert _sup(q, k, v, m, dst.half()) == (True, 0)                                 # F16 dst: a fused cast
@@ -234,3 +242,54 @@ def test_norm_descriptor_checks():
     assert ask(kd_fa.qk_norm(w[1:129], w[:128])) == (False, kd_fa.ERR_LAYOUT)     # 4-byte aligned weight
     assert ask(kd_fa.qk_norm(w[:128], w[:128], float("nan"))) == (False, kd_fa.ERR_ROPE)
     assert ask(kd_fa.qk_norm(w[:128], w[:128], -1.0)) == (False, kd_fa.ERR_ROPE)
+
+
+def test_f32_k_supports_agrees_with_run():
+    """kd_fa_dit_supports accepts an F32 K (the projection output) only when K
+    is transformed -- normalised or rotated -- and kd_fa_dit_run then needs
+    the workspace whose pre-pass rounds it; both answers are given before
+    any device work, so they are checked here on the host."""
+    q, k, v, m, dst = _node(Lq=60, Lk=60, qt=torch.float32, kt=torch.bfloat16)
+    k32 = k.float()
+    w = torch.ones(128)
+    lib = kd_fa.lib()
+
+    def ask(rope, norm):
+        d = kd_fa.make_desc(q, k32, v, None, dst, 0.1)
+        reason = ctypes.c_int(0)
+        ok = lib.kd_fa_dit_supports(ctypes.byref(d), ctypes.byref(rope) if rope is not None else None,
+                                    ctypes.byref(norm) if norm is not None else None, ctypes.byref(reason))
+        run = lib.kd_fa_dit_run(ctypes.byref(d), ctypes.byref(rope) if rope is not None else None,
+                                ctypes.byref(norm) if norm is not None else None, None, 0, None)
+        return bool(ok), reason.value, run
+
+    table = kd_fa.rope_table(torch.zeros((60, 128)))
+    # no K transform: F32 K is not an operand type of the node
+    assert ask(None, None) == (False, kd_fa.ERR_TYPE, kd_fa.ERR_TYPE)
+    assert ask(None, kd_fa.qk_norm(w, None)) == (False, kd_fa.ERR_TYPE, kd_fa.ERR_TYPE)
+    # K transformed: supported, and the run without a workspace says so
+    assert ask(table, None) == (True, 0, kd_fa.ERR_NULL)
+    assert ask(None, kd_fa.qk_norm(None, w)) == (True, 0, kd_fa.ERR_NULL)
+
+
+def test_routing_hook_round_trips():
+    """kd_fa_set_routing is process-wide and returns the previous flags; the
+    context manager restores them."""
+    lib = kd_fa.lib()
+    assert lib.kd_fa_set_routing(kd_fa.ROUTE_DEFAULT) == kd_fa.ROUTE_DEFAULT
+    with kd_fa.routing(kd_fa.ROUTE_NO_W64 | kd_fa.ROUTE_NO_XRES):
+        assert lib.kd_fa_set_routing(kd_fa.ROUTE_NO_W64 | kd_fa.ROUTE_NO_XRES) == \
+            kd_fa.ROUTE_NO_W64 | kd_fa.ROUTE_NO_XRES
+    assert lib.kd_fa_set_routing(kd_fa.ROUTE_DEFAULT) == kd_fa.ROUTE_DEFAULT
+
+
+def test_product_reads_no_environment():
+    """Kernel choice is a function of the node (and the routing hook) only:
+    the shipped library and the loop generator read no environment."""
+    import re
+    csrc = os.path.join(ROOT, "kandinsky.cpp_amd", "csrc")
+    for name in os.listdir(csrc):
+        if name.endswith((".cpp", ".hip", ".h", ".py")):
+            with open(os.path.join(csrc, name)) as f:
+                text = f.read()
+            assert not re.search(r"\bgetenv\b|os\.environ", text), name

@@ -104,16 +104,8 @@ def test_d512_vae_64x64_sampled():
 
 def _run_rows32(q, k, v, **kw):
     """The same call with 32 query rows per workgroup forced."""
-    import os
-    old = os.environ.get("KD_FA_D512_ROWS")
-    os.environ["KD_FA_D512_ROWS"] = "32"
-    try:
+    with kd_fa.routing(kd_fa.ROUTE_D512_R1):
         return _run(q, k, v, **kw)
-    finally:
-        if old is None:
-            del os.environ["KD_FA_D512_ROWS"]
-        else:
-            os.environ["KD_FA_D512_ROWS"] = old
 
 
 ROWS64_CASES = [

@@ -136,10 +136,11 @@ def test_self_attention_f32_k_through_workspace():
     q2 = _rot(_norm(q, wq), table, torch.bfloat16)
     assert torch.equal(ws.view(k.shape).cpu(), k2)
     assert torch.equal(out, _plain(q2, k2, v))
-    # an F32 K needs the workspace: the on-load path works in the operand type
+    # an F32 K needs the workspace (the on-load path works in the operand type):
+    # without one the call names the missing buffer
     with pytest.raises(kd_fa.KdFaError) as e:
         kd_fa.flash_attn_ext(qg, kg, vg, rope=rope, norm=norm)
-    assert e.value.status == kd_fa.ERR_TYPE
+    assert e.value.status == kd_fa.ERR_NULL
     assert_parity(gather_rows(out, np.arange(B * H * L), H, L), orc.fa_f64(q2, k2, v), "dit F32 K")
 
 

@@ -2,7 +2,8 @@
 unmasked calls whose K is read as stored and whose Lk is a multiple of 64.
 
 Each case runs twice through the C ABI: once as routed (fa_fwd_w64) and once
-with KD_FA_W64=0 (the 32-row kernel, fa_fwd_d128), and the two outputs must
+with the 64-row kernel routed out (kd_fa_set_routing: the 32-row kernel,
+fa_fwd_d128), and the two outputs must
 be bitwise equal -- both kernels perform the same arithmetic per query row.
 Parity against the float64 oracle completes each case.  The shapes walk the
 loop's control paths: 1 key tile (last step only), 2 (one step + last), 3
@@ -10,8 +11,6 @@ loop's control paths: 1 key tile (last step only), 2 (one step + last), 3
 batch broadcast; strided activation views; F16 and BF16; scales that force
 the running-max rescale in later tiles.
 """
-import os
-
 import numpy as np
 import pytest
 import torch
@@ -36,12 +35,9 @@ def _announce(msg):
 
 def _both(fn):
     """(routed output, 32-row kernel output) of fn()."""
-    os.environ["KD_FA_W64"] = "0"
-    try:
+    with kd_fa.routing(kd_fa.ROUTE_NO_W64):
         ref = fn()
         torch.cuda.synchronize()
-    finally:
-        del os.environ["KD_FA_W64"]
     out = fn()
     torch.cuda.synchronize()
     return out, ref

@@ -3,7 +3,8 @@ with Lk <= 256 whose K is read as stored and whose Q is not rotated -- the
 text cross-attention (src/models/crossdit.hpp:174-200).
 
 Each case runs twice through the C ABI: once as routed (fa_fwd_xres) and
-once with KD_FA_XRES=0 (the 32-row kernel, fa_fwd_d128); the outputs must be
+once with the short-key kernel routed out (kd_fa_set_routing: the 32-row
+kernel, fa_fwd_d128); the outputs must be
 bitwise equal, since both kernels perform the same arithmetic per query row.
 Parity against the float64 oracle completes each case.  The shapes walk the
 kernel's structure: 1..4 key tiles held in LDS with ragged last tiles
@@ -14,7 +15,6 @@ every row (skipped) and rows that see no key, F32 Q (the reference's
 operand type), the query/key RMSNorm path, negative / zero scales, and
 16-bit outputs.
 """
-import os
 
 import numpy as np
 import pytest
@@ -41,12 +41,9 @@ def _announce(msg):
 
 def _both(fn):
     """(routed output, 32-row kernel output) of fn()."""
-    os.environ["KD_FA_XRES"] = "0"
-    try:
+    with kd_fa.routing(kd_fa.ROUTE_NO_XRES):
         ref = fn()
         torch.cuda.synchronize()
-    finally:
-        del os.environ["KD_FA_XRES"]
     out = fn()
     torch.cuda.synchronize()
     return out, ref
