@@ -72,7 +72,9 @@ enum {
     KD_FA_ERR_PARAM      = -5,   /* max_bias, softcap, sinks or scale unsupported */
     KD_FA_ERR_ROPE       = -6,   /* invalid RoPE or norm descriptor       */
     KD_FA_ERR_LAUNCH     = -7,   /* HIP launch failed                     */
-    KD_FA_ERR_DEVICE     = -8    /* no gfx950 device / runtime error      */
+    KD_FA_ERR_DEVICE     = -8,   /* no gfx950 device / runtime error      */
+    KD_FA_ERR_SCRATCH    = -9    /* K exceeds the static scratch of
+                                    kd_fa_dit_run_static                  */
 };
 
 /* A ggml tensor view: struct ggml_tensor's type, ne, nb and data. */
@@ -257,6 +259,26 @@ int kd_fa_rope_axes_fill(int T, int Hp, int Wp, const int axes[3],
  * with: out[pos][D] interleaved (cos, sin) of pos * freq_i.
  */
 int kd_fa_rope_text_table(int L, int D, float theta, float *out);
+
+/*
+ * kd_fa_dit_run_static - kd_fa_dit_run with the K workspace taken from a
+ * device array of the library instead of a caller buffer.  It has no
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under stream capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  The caller passes inputs and outputs only; the
+ * library allocates nothing, and the array (KD_FA_STATIC_SCRATCH_BYTES per
+ * GPU, held until the process ends) is set up on the first call on each
+ * device.  A node whose transformed K (the kd_fa_rope_workspace_size bytes)
+ * exceeds the array is refused with KD_FA_ERR_SCRATCH before any device
+ * work; a node that transforms no K needs no workspace and always runs.
+ * The result is bitwise equal to kd_fa_dit_run's with a caller workspace.
+ * Every call on a GPU shares that GPU's array: calls that overlap on one
+ * GPU (two streams, two host threads) race and must be serialised by the
+ * caller.
+ */
+#define KD_FA_STATIC_SCRATCH_BYTES ((size_t)64 << 20)
+int kd_fa_dit_run_static(const kd_fa_desc *desc, const kd_fa_rope *rope, const kd_fa_qk_norm *norm,
+                         void *stream);
 
 /*
  * kd_fa_set_routing - comparison hook for tests and tuning; it has no

@@ -312,6 +312,18 @@ bool axes_ok(int T, int Hp, int Wp, const int axes[3]) {
 
 namespace kdfa {
 int device_gfx950() { return device_ok(); }
+
+int run_node(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *ws, size_t ws_bytes,
+             void *stream) {
+    return run(d, r, n, ws, ws_bytes, stream);
+}
+
+size_t k_workspace_need(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, int *status) {
+    const bool k_xform = (r && r->mode != KD_FA_ROPE_NONE) || (n && n->k_weight);
+    *status = validate(d, r, n, nullptr, k_xform);
+    if (*status != KD_FA_OK || !k_xform || d->q.ne[0] != kHeadDim) return 0;
+    return rope_ws_bytes(d);
+}
 }  // namespace kdfa
 
 extern "C" {
@@ -440,6 +452,7 @@ const char *kd_fa_strerror(int status) {
     case KD_FA_ERR_ROPE: return "invalid RoPE descriptor";
     case KD_FA_ERR_LAUNCH: return "HIP kernel launch failed";
     case KD_FA_ERR_DEVICE: return "current device is not a gfx950 GPU";
+    case KD_FA_ERR_SCRATCH: return "transformed K larger than the library's static scratch (KD_FA_STATIC_SCRATCH_BYTES)";
     default: return "unknown status";
     }
 }

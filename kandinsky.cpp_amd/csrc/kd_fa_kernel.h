@@ -51,6 +51,14 @@ struct Args {
 // else KD_FA_ERR_DEVICE.
 int device_gfx950();
 
+// kd_fa_dit_run's body: validation, kernel choice and launch(es).
+int run_node(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *ws, size_t ws_bytes,
+             void *stream);
+
+// Bytes of K-sized workspace the node needs (0 when K is not transformed);
+// *status gets the node's validation status (host-only).
+size_t k_workspace_need(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, int *status);
+
 // Enqueue the forward kernel for K/V element type kv_type on `stream`.
 // Q is normalised (qn_w) and rotated (RoPE mode) on load; K too (kn_w,
 // RoPE mode) when k_rope.

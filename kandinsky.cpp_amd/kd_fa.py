@@ -49,6 +49,8 @@ ERR_PARAM = -5
 ERR_ROPE = -6
 ERR_LAUNCH = -7
 ERR_DEVICE = -8
+ERR_SCRATCH = -9
+STATIC_SCRATCH_BYTES = 64 << 20
 
 # kd_fa_set_routing flags (comparison hooks for tests and tuning)
 ROUTE_DEFAULT = 0
@@ -158,6 +160,8 @@ def _lib():
         lib.kd_fa_strerror.restype = ctypes.c_char_p
         lib.kd_fa_version.argtypes = []
         lib.kd_fa_version.restype = ctypes.c_int
+        lib.kd_fa_dit_run_static.argtypes = [P(KdFaDesc), P(KdFaRope), P(KdFaQkNorm), ctypes.c_void_p]
+        lib.kd_fa_dit_run_static.restype = ctypes.c_int
         lib.kd_fa_set_routing.argtypes = [ctypes.c_int]
         lib.kd_fa_set_routing.restype = ctypes.c_int
         _LIB = lib
@@ -336,6 +340,21 @@ def run_desc(desc: KdFaDesc, rope: KdFaRope | None = None, stream=None, workspac
                                         ctypes.c_void_p(workspace.data_ptr()), nbytes,
                                         ctypes.c_void_p(handle))
     return _lib().kd_fa_rope_run(ctypes.byref(desc), ctypes.byref(rope), ctypes.c_void_p(handle))
+
+
+def run_static(desc: KdFaDesc, rope: KdFaRope | None = None, norm: KdFaQkNorm | None = None, stream=None) -> int:
+    """kd_fa_dit_run_static: kd_fa_dit_run with the K workspace in the
+    library's static device array (no allocation by anyone).  Returns the
+    status code."""
+    torch = _torch()
+    if stream is None:
+        handle = torch.cuda.current_stream().cuda_stream
+    elif isinstance(stream, int):
+        handle = stream
+    else:
+        handle = stream.cuda_stream
+    return _lib().kd_fa_dit_run_static(ctypes.byref(desc), ctypes.byref(rope) if rope is not None else None,
+                                       ctypes.byref(norm) if norm is not None else None, ctypes.c_void_p(handle))
 
 
 def workspace_size(desc: KdFaDesc) -> int:

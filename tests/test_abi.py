@@ -73,7 +73,7 @@ def test_header_compiles_as_c_and_cxx():
 def test_version_and_strerror():
     lib = kd_fa.lib()
     assert lib.kd_fa_version() >= 100
-    for code in range(0, -9, -1):
+    for code in range(0, -10, -1):
         assert lib.kd_fa_strerror(code)
     assert b"unknown" in lib.kd_fa_strerror(-99)
 
@@ -293,3 +293,23 @@ def test_product_reads_no_environment():
             with open(os.path.join(csrc, name)) as f:
                 text = f.read()
             assert not re.search(r"\bgetenv\b|os\.environ", text), name
+
+
+def test_static_entry_point_refuses_oversize_k_before_device_work():
+    """kd_fa_dit_run_static checks the transformed K against its static
+    scratch (KD_FA_STATIC_SCRATCH_BYTES) on the host, before any device
+    call: a K one row over the limit is refused with KD_FA_ERR_SCRATCH, an
+    invalid node with its own reason."""
+    lib = kd_fa.lib()
+    L = kd_fa.STATIC_SCRATCH_BYTES // (128 * 2) + 1          # one bf16 K row over
+    q = torch.zeros((1, 1, 4, 128), dtype=torch.bfloat16)
+    k = torch.zeros((1, 1, L, 128), dtype=torch.bfloat16)
+    dst = torch.zeros((1, 4, 1, 128), dtype=torch.float32)
+    d = kd_fa.make_desc(q, k, k, None, dst, 0.1)
+    tab = torch.zeros((L, 128))
+    rope = kd_fa.rope_table(tab)
+    assert kd_fa.workspace_size(d) == kd_fa.STATIC_SCRATCH_BYTES + 256
+    assert lib.kd_fa_dit_run_static(ctypes.byref(d), ctypes.byref(rope), None, None) == kd_fa.ERR_SCRATCH
+    bad = kd_fa.make_desc(q, k, k, None, dst, 0.1, max_bias=1.0)
+    assert lib.kd_fa_dit_run_static(ctypes.byref(bad), ctypes.byref(rope), None, None) == kd_fa.ERR_PARAM
+    assert b"static scratch" in lib.kd_fa_strerror(kd_fa.ERR_SCRATCH)
