@@ -289,6 +289,18 @@ static int check_desc(const kd_fa_desc *d, const kd_fa_rope *r, int need_dst) {
     return KD_FA_OK;
 }
 
+/* Worker threads when the caller asks for the default: the CPU share the
+   environment grants (OMP_NUM_THREADS, as a one-GPU job is given), else
+   every online core. */
+static int default_threads(void) {
+    const char *e = getenv("OMP_NUM_THREADS");
+    if (e) {
+        const int n = atoi(e);
+        if (n > 0) return n;
+    }
+    return (int)sysconf(_SC_NPROCESSORS_ONLN);
+}
+
 typedef struct {
     const kd_fa_desc *d;
     const kd_fa_rope *r;     /* NULL or mode NONE: no rotation */
@@ -509,7 +521,7 @@ static int run(const kd_fa_desc *d, const kd_fa_rope *r, int f16_vacc, int f64,
     for (int64_t x = 0; x < n; ++x) { order[x] = ents[x].ir; slot[x] = ents[x].slot; }
     free(ents);
 
-    if (n_threads <= 0) n_threads = (int)sysconf(_SC_NPROCESSORS_ONLN);
+    if (n_threads <= 0) n_threads = default_threads();
     if (n_threads < 1) n_threads = 1;
     if (n_threads > n) n_threads = (int)n;
 
