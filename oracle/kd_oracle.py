@@ -18,7 +18,8 @@ import numpy as np
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libkd_oracle.so")
+# KD_ORACLE_LIB selects another build of the same library (the sanitized one)
+LIB_PATH = os.environ.get("KD_ORACLE_LIB") or os.path.join(_HERE, "libkd_oracle.so")
 
 TYPE_F32, TYPE_F16, TYPE_BF16 = 0, 1, 30
 ROPE_NONE, ROPE_TABLE, ROPE_AXES = 0, 1, 2

@@ -11,6 +11,11 @@ import tempfile
 import kd_fa
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+# tests/run_sanitized.sh: the mirror is compiled under ASan + UBSan as well,
+# with the compiler whose runtime the sanitized library uses
+SANITIZE = os.environ.get("KD_SANITIZE") == "1"
+CXX = (["/opt/rocm/llvm/bin/clang++", "-fsanitize=address,undefined", "-fno-sanitize-recover=undefined",
+        "-shared-libsan", "-g"] if SANITIZE else ["g++"])
 
 SRC = r"""
 #include <cstdio>
@@ -53,7 +58,7 @@ def test_ops_attention_mirror_builds_views():
         exe = os.path.join(d, "t")
         with open(src, "w") as f:
             f.write(SRC)
-        subprocess.run(["g++", "-std=c++17", "-Wall", "-Werror",
+        subprocess.run(CXX + ["-std=c++17", "-Wall", "-Werror",
                         "-I", os.path.join(ROOT, "kandinsky.cpp_amd", "host"), src,
                         "-L", lib_dir, "-lkd_fa", f"-Wl,-rpath,{lib_dir}", "-o", exe], check=True)
         out = subprocess.run([exe], capture_output=True, text=True)
