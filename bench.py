@@ -52,6 +52,9 @@ def parse():
                         "and print its ms per call (for counter runs)")
     p.add_argument("--cross-only", action="store_true",
                    help="only the text cross-attention (C2 shape): for counter runs of its kernel")
+    p.add_argument("--hbm-ceiling", action="store_true",
+                   help="only the HBM streaming probes (libkd_probe.so) at the cross-attention's sizes: "
+                        "bf16 -> F32 widening (its Q-in / O-out byte mix), read-only, write-only")
     return p.parse_args()
 
 
@@ -202,6 +205,45 @@ def self_check(torch, q, k, v, table, out, scale, rows_per_head=4, seed=11):
             "reference": "torch float64 on the GPU, same rounded operands (not the oracle)"}
 
 
+def hbm_ceiling(torch, dev, stream):
+    """What this GPU sustains for the cross-attention's byte mix: a bf16 array
+    of the C2 query size (520 MB) widened to F32 (1.04 GB written), read-only
+    and write-only streams of the same arrays; best over launch sizes, the
+    mean of 20 launches each (HIP events on the launch stream)."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "kandinsky.cpp_amd", "libkd_probe.so"))
+    lib.kd_probe_widen.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                   ctypes.c_void_p]
+    lib.kd_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+    lib.kd_probe_write.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+    n = 2 * HEADS * 31744 * D
+    src = torch.ones(n, dtype=torch.bfloat16, device=dev)
+    dst = torch.empty(n, dtype=torch.float32, device=dev)
+    sink = torch.empty(65536 * 4, dtype=torch.int32, device=dev)
+    h = ctypes.c_void_p(stream.cuda_stream)
+    n16 = n * 2 // 16
+    res = {"bytes_read": n * 2, "bytes_written": n * 4}
+    widen = [(f"widen_bf16_to_f32_u{v % 10}{'_nt' if v > 10 else ''}",
+              (lambda v: lambda g: lib.kd_probe_widen(src.data_ptr(), dst.data_ptr(), n16, g, v, h))(v), n * 6)
+             for v in (1, 4, 8, 11, 14, 18)]
+    for name, fn, nbytes in widen + [
+            ("read", lambda g: lib.kd_probe_read(dst.data_ptr(), sink.data_ptr(), n * 4 // 16, g, h), n * 4),
+            ("write", lambda g: lib.kd_probe_write(dst.data_ptr(), n * 4 // 16, g, h), n * 4)]:
+        best = None
+        for g in (1024, 2048, 4096, 8192, 16384):
+            ms = time_launches(torch, lambda: fn(g), 20, 3, stream)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            if best is None or gbs > best[1]:
+                best = (g, gbs, ms)
+        res[name] = {"GBps": round(best[1], 1), "ms": round(best[2], 4), "blocks": best[0],
+                     "frac_of_8TBps": round(best[1] / PEAK_HBM_GBS, 4)}
+    # torch's own widening copy for comparison
+    dv = dst.view(-1)
+    ms = time_launches(torch, lambda: dv.copy_(src), 20, 3, stream)
+    res["torch_copy_bf16_to_f32"] = {"GBps": round(n * 6 / (ms * 1e-3) / 1e9, 1), "ms": round(ms, 4)}
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -223,6 +265,9 @@ def main():
         print(json.dumps({"copy_calibration_bytes": src.numel() * 4, "copies": 3}))
         return
     stream = torch.cuda.current_stream()
+    if args.hbm_ceiling:
+        print(json.dumps(hbm_ceiling(torch, dev, stream)), flush=True)
+        return
     B, T, Hp, Wp = 2, 31, 32, 32
     L = T * Hp * Wp
     bf = torch.bfloat16
@@ -362,11 +407,11 @@ def main():
         sec["cross_attn_GBps"] = round(bytes2 / (ms2 * 1e-3) / 1e9, 1)
         sec["cross_attn_hbm_frac"] = round(bytes2 / (ms2 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
         # the reference's own cross-attention operand form (ops.hpp:122-169,
-        # crossdit.hpp:198): Q F32, K/V F16, no mask, prompt lengths 300 and
-        # 512 (the longest after the tokenizer's crop)
+        # crossdit.hpp:198): Q F32, K/V F16, no mask, prompt lengths 77, 300
+        # and 512 (the longest after the tokenizer's crop)
         q32 = rand(torch, (B, HEADS, L, D), 3, dev, torch.float32)
         o32 = torch.empty((B, L, HEADS, D), device=dev, dtype=torch.float32)
-        for Lk in (300, 512):
+        for Lk in (77, 300, 512):
             kf = rand(torch, (B, HEADS, Lk, D), 1100 + Lk, dev, torch.float16)
             vf = rand(torch, (B, HEADS, Lk, D), 2100 + Lk, dev, torch.float16)
             df = kd_fa.make_desc(q32, kf, vf, None, o32, 1.0 / D ** 0.5)

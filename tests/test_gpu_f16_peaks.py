@@ -175,3 +175,20 @@ def test_peaks_reference_operand_form_production_shape():
     rows = np.union1d(_planted_rows(planted, H, L), sample_rows(B, H, L, 64, seed=78))
     m = _check(out, q, k, v, rows, H, L, "production peaks")
     print(f"[peaks production] {m}", flush=True)
+
+
+@pytest.mark.parametrize("Lk", [300, 512])
+def test_cross_attention_reference_form_long_prompt(Lk):
+    """The text cross-attention as the reference builds it for a long prompt
+    (Lk up to 512 after the tokenizer's crop, qwen_tokenizer.hpp:129,183):
+    Q F32 [128, 31744, 32], K/V F16 [128, Lk, 32], no mask; 64 sampled rows
+    per head, with peaks planted for every 97th row."""
+    _need_gpu()
+    B, H, L = 1, HEADS, 31744
+    _announce(f"cross-attn reference form: Q F32 [128,{L},{H}], K/V F16 Lk={Lk}, unmasked")
+    q, k, v, planted = spiked(B, H, L, Lk, torch.float16, seed=Lk + 7, every=97)
+    out = kd_fa.flash_attn_ext(q.to(DEV), k.to(DEV), v.to(DEV))
+    torch.cuda.synchronize()
+    rows = np.union1d(sample_rows(B, H, L, 64, seed=Lk), _planted_rows(planted, H, L)[::8])
+    m = _check(out, q, k, v, rows, H, L, f"cross Lk={Lk}")
+    print(f"[cross Lk={Lk}] {m}", flush=True)
