@@ -353,12 +353,15 @@ def main():
 
     if not args.no_secondary:
         sec = {}
-        # the same pass as one kernel without a workspace (kd_fa_rope_run): K
-        # tiles rotated on their way into LDS by every query tile; bitwise equal
+        # the same pass without a workspace (kd_fa_rope_run): K rotated by the
+        # pre-pass into output rows that a later head group overwrites, the
+        # 64-row kernel group by group, the last group rotating K on load;
+        # bitwise equal
         ms_f = time_launches(torch, lambda: kd_fa.run_desc(desc, rope, stream), args.steps, args.warmup, stream)
         sec["self_attn_fused_ms"] = round(ms_f, 4)
         sec["self_attn_fused_tflops"] = round(flop / (ms_f * 1e-3) / 1e12, 2)
-        sec["self_attn_fused_note"] = "kd_fa_rope_run: Q and K rotated on load in one kernel, no workspace"
+        sec["self_attn_fused_note"] = ("kd_fa_rope_run, no workspace: K staged in output rows of later head "
+                                       "groups, the last group rotating K on load")
         # the attention alone on unrotated operands (kd_fa_run)
         ms_n = time_launches(torch, lambda: kd_fa.run_desc(desc, None, stream), args.steps, args.warmup, stream)
         sec["self_attn_norope_ms"] = round(ms_n, 4)

@@ -196,6 +196,85 @@ static void xres_split(kdfa::Args &a) {
     a.n_blocks = (int32_t)(a.n_qt * bh);
 }
 
+// Staged calls: K transformed (normalised and / or rotated) without a
+// workspace.  Rotating K on load costs every query tile of a head the whole
+// rotation again; instead the (b, h) pairs are processed in groups, and each
+// group's transformed K is written by the pre-pass into the output rows of
+// the NEXT group -- rows that group's attention overwrites only later, in
+// stream order -- so that the group runs on the 64-row kernel with K read as
+// stored.  A transformed K row (256 bytes) takes half of an F32 output row,
+// so a group may hold up to twice as many heads as the next (as many, for a
+// 16-bit output); the sizes shrink geometrically towards the last group
+// (one or two heads), which has no later rows to borrow and rotates K on
+// load.  The transformed values are the pre-pass's, so the result is
+// bitwise that of the workspace path.  Groups stay within one batch.
+bool staged_ok(const kdfa::Args &a, const kd_fa_desc *d, int route) {
+    if ((route & KD_FA_ROUTE_NO_W64) || a.m) return false;
+    if (a.rk2 != 1 || a.rk3 != 1 || a.rv2 != 1 || a.rv3 != 1) return false;
+    if (a.Lk < 64 || a.Lk % 64 != 0 || a.Lq < a.Lk) return false;
+    const int64_t row = kHeadDim * (int64_t)elem_size(d->dst.type);
+    if ((int64_t)d->dst.nb[1] != row) return false;   // the heads of an output row are contiguous
+    if ((int64_t)a.H * a.B < 4) return false;
+    const int64_t lim = (int64_t)1 << 31;            // the 64-row kernel's 32-bit buffer offsets
+    return (int64_t)(a.Lk - 1) * (int64_t)d->dst.nb[2] + 256 < lim && (int64_t)(a.Lk - 1) * a.v_nb1 + 256 < lim;
+}
+
+// a's view restricted to heads [h0, h0 + n) of batch b (no broadcast)
+kdfa::Args head_range(const kdfa::Args &a, int b, int h0, int n) {
+    kdfa::Args s = a;
+    s.q = a.q + (int64_t)b * a.q_nb3 + (int64_t)h0 * a.q_nb2;
+    s.k = a.k + (int64_t)b * a.k_nb3 + (int64_t)h0 * a.k_nb2;
+    s.v = a.v + (int64_t)b * a.v_nb3 + (int64_t)h0 * a.v_nb2;
+    s.o = a.o + (int64_t)b * a.o_nb3 + (int64_t)h0 * a.o_nb1;
+    s.H = n;
+    s.B = 1;
+    return s;
+}
+
+int run_staged(const kdfa::Args &a, int kv_type, hipStream_t hs) {
+    const int H = a.H, P = a.H * a.B;
+    const int ratio = a.o_type == KD_FA_TYPE_F32 ? 2 : 1;   // transformed K rows per output row
+    const int n_last = std::min(P >= 16 ? 2 : 1, H);
+    // group sizes from the last backwards: each at most `ratio` times the
+    // next, within the batch of its pairs
+    std::vector<int> start;
+    {
+        int end = P - n_last, next = n_last;
+        while (end > 0) {
+            const int b = (end - 1) / H;
+            const int n = std::min(end - b * H, ratio * next);
+            start.push_back(end - n);
+            next = n;
+            end -= n;
+        }
+        std::reverse(start.begin(), start.end());
+        start.push_back(P - n_last);
+        start.push_back(P);
+    }
+    const int n_groups = (int)start.size() - 1;   // the last one rotates K on load
+    const int64_t krow = kHeadDim * (int64_t)elem_size(kv_type);
+    for (int g = 0; g + 1 < n_groups; ++g) {
+        const int p0 = start[g], n = start[g + 1] - p0;
+        const int p1 = start[g + 1];   // the next group: its output rows hold this group's K
+        kdfa::Args s = head_range(a, p0 / H, p0 % H, n);
+        char *kst = a.o + (int64_t)(p1 / H) * a.o_nb3 + (int64_t)(p1 % H) * a.o_nb1;
+        const kdfa::KStrides st = {a.o_nb2, krow, 0};
+        if (kdfa::launch_rope_k(s, kv_type, n, 1, kst, st, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
+        s.k = kst;
+        s.k_nb1 = a.o_nb2;
+        s.k_nb2 = krow;
+        s.k_nb3 = 0;
+        s.n_qt = (a.Lq + kdfa::block_rows(false, false) - 1) / kdfa::block_rows(false, false);
+        s.n_blocks = s.n_qt * n;
+        if (kdfa::launch_w64(s, kv_type, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
+    }
+    const int p0 = start[n_groups - 1];
+    kdfa::Args s = head_range(a, p0 / H, p0 % H, n_last);
+    s.n_qt = (a.Lq + kdfa::block_rows(false, true) - 1) / kdfa::block_rows(false, true);
+    s.n_blocks = s.n_qt * n_last;
+    return kdfa::launch(s, kv_type, true, hs) == hipSuccess ? KD_FA_OK : KD_FA_ERR_LAUNCH;
+}
+
 int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *ws, size_t ws_bytes,
         void *stream) {
     bool mask_vec = false;
@@ -267,6 +346,7 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
         return kdfa::launch_d512(a, d->v.type, rows, hs) == hipSuccess ? KD_FA_OK : KD_FA_ERR_LAUNCH;
     }
     bool k_rope = k_xform && !ws;
+    if (k_rope && staged_ok(a, d, route)) return run_staged(a, d->v.type, hs);
     const int rows = kdfa::block_rows(a.m != nullptr, k_rope);
     a.n_qt = (int32_t)((Lq + rows - 1) / rows);
     a.n_blocks = (int32_t)(a.n_qt * H * B);
@@ -277,8 +357,9 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
 
     if (ws && k_xform) {
         const int hk = (int)d->k.ne[2], bk = (int)d->k.ne[3];
-        if (kdfa::launch_rope_k(a, d->v.type, hk, bk, ws, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
         const int64_t row = kHeadDim * (int64_t)elem_size(d->v.type);
+        const kdfa::KStrides st = {row, row * a.Lk, row * a.Lk * hk};
+        if (kdfa::launch_rope_k(a, d->v.type, hk, bk, ws, st, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
         a.k = static_cast<const char *>(ws);
         a.k_nb1 = row;
         a.k_nb2 = row * a.Lk;

@@ -79,9 +79,16 @@ hipError_t launch_xres(const Args &a, int kv_type, hipStream_t stream);
 // those)
 hipError_t launch_d512(const Args &a, int kv_type, int rows, hipStream_t stream);
 
+// Byte strides of the transformed K the pre-pass writes: per key, per K
+// head, per K batch (contiguous [D, Lk, Hk, Bk]: 256, 256 Lk, 256 Lk Hk).
+struct KStrides {
+    int64_t key, head, batch;
+};
+
 // Normalise (kn_w) and rotate (RoPE mode) K ([D, Lk, H/rk2, B/rk3] through
-// a.k and its strides) into `out`, contiguous, in K's type.
-hipError_t launch_rope_k(const Args &a, int kv_type, int k_heads, int k_batch, void *out, hipStream_t stream);
+// a.k and its strides) into `out` with strides `st`, in K's type.
+hipError_t launch_rope_k(const Args &a, int kv_type, int k_heads, int k_batch, void *out, const KStrides &st,
+                         hipStream_t stream);
 
 // Waves per workgroup (32 query rows each): 8 (two waves per SIMD) for the
 // unmasked kernels; 4 for the plain masked one -- the short text

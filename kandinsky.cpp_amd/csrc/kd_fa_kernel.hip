@@ -1391,13 +1391,15 @@ hipError_t launch(const Args &a, int kv_type, bool k_rope, hipStream_t stream) {
 // ---------------------------------------------------------------------------
 // K pre-pass of the workspace entry points: ops::rms_norm (kn_w) and
 // rope::apply (src/rope.hpp:109-155) on K with the same F32 arithmetic as the
-// in-kernel transform, rounded to K's type, written to a contiguous
-// [D, Lk, Hkv, Bk] buffer in the operand type T (K may be stored in F32).
+// in-kernel transform, rounded to K's type, written in the operand type T (K
+// may be stored in F32) to out + key * o.key + head * o.head + batch *
+// o.batch: a contiguous [D, Lk, Hkv, Bk] workspace, or rows of the call's
+// own output buffer that the attention writes later (the staged path).
 // One thread per 8-element chunk; the 16 chunks of a row are 16 consecutive
 // lanes, which reduce the row's squares together.
 // ---------------------------------------------------------------------------
 template <typename T, int RM>
-__global__ __launch_bounds__(256) void rope_k_kernel(Args a, char *out, int64_t n_chunks) {
+__global__ __launch_bounds__(256) void rope_k_kernel(Args a, char *out, KStrides o, int64_t n_chunks) {
     typedef Elem<T> E;
     const int hk = a.H / a.rk2;   // K heads
     // n_chunks is a multiple of 16 and so is every lane group's first index:
@@ -1424,35 +1426,37 @@ __global__ __launch_bounds__(256) void rope_k_kernel(Args a, char *out, int64_t 
             rotate8(x, *reinterpret_cast<const f32x4 *>(cp), *reinterpret_cast<const f32x4 *>(cp + 4));
         }
         for (int e = 0; e < 4; ++e) w[e] = E::pack2(x[2 * e], x[2 * e + 1]);
-        *reinterpret_cast<u32x4 *>(out + i * 16) = w;
+        *reinterpret_cast<u32x4 *>(out + (int64_t)key * o.key + (int64_t)h * o.head + (int64_t)b * o.batch + c * 16) = w;
     }
 }
 
 template <typename T>
-static void launch_rope_k_t(const Args &a, int grid, char *o, int64_t n_chunks, hipStream_t stream) {
+static void launch_rope_k_t(const Args &a, int grid, char *o, const KStrides &st, int64_t n_chunks,
+                            hipStream_t stream) {
     switch (a.rope_mode) {
     case KD_FA_ROPE_TABLE:
-        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_TABLE>), dim3(grid), dim3(256), 0, stream, a, o, n_chunks);
+        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_TABLE>), dim3(grid), dim3(256), 0, stream, a, o, st, n_chunks);
         break;
     case KD_FA_ROPE_AXES:
-        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_AXES>), dim3(grid), dim3(256), 0, stream, a, o, n_chunks);
+        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_AXES>), dim3(grid), dim3(256), 0, stream, a, o, st, n_chunks);
         break;
     default:
-        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_NONE>), dim3(grid), dim3(256), 0, stream, a, o, n_chunks);
+        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_NONE>), dim3(grid), dim3(256), 0, stream, a, o, st, n_chunks);
         break;
     }
 }
 
-hipError_t launch_rope_k(const Args &a, int kv_type, int k_heads, int k_batch, void *out, hipStream_t stream) {
+hipError_t launch_rope_k(const Args &a, int kv_type, int k_heads, int k_batch, void *out, const KStrides &st,
+                         hipStream_t stream) {
     const int64_t n_chunks = (int64_t)a.Lk * k_heads * k_batch * 16;
     if (n_chunks == 0) return hipSuccess;
     const int64_t want = (n_chunks + 255) / 256;
     const int grid = (int)(want < 65536 ? want : 65536);
     char *o = static_cast<char *>(out);
     if (kv_type == KD_FA_TYPE_BF16)
-        launch_rope_k_t<__bf16>(a, grid, o, n_chunks, stream);
+        launch_rope_k_t<__bf16>(a, grid, o, st, n_chunks, stream);
     else
-        launch_rope_k_t<_Float16>(a, grid, o, n_chunks, stream);
+        launch_rope_k_t<_Float16>(a, grid, o, st, n_chunks, stream);
     return hipGetLastError();
 }
 
