@@ -396,6 +396,22 @@ def main():
             sec[f"self_attn_{tag}_tflops"] = round(flx / (msx * 1e-3) / 1e12, 2)
             sec[f"self_attn_{tag}_pct_bf16_peak"] = round(100.0 * flx / (msx * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2)
             del qx, kx, vx, ox, wsx
+        # a token count that is not a multiple of 64: 768x432, 121 frames ->
+        # latent 31 x 54 x 96, patch (1, 2, 2) -> 31 x 27 x 48 = 40,176 tokens,
+        # batch 2, with and without the K workspace
+        Tr, Hr, Wr = 31, 27, 48
+        Lr = Tr * Hr * Wr
+        qr, kr, vr = (rand(torch, (B, HEADS, Lr, D), 70 + j, dev, bf) for j in range(3))
+        orr = torch.empty((B, Lr, HEADS, D), device=dev, dtype=torch.float32)
+        ropr = kd_fa.rope_table(torch.from_numpy(kd_fa.visual_rope_table(Tr, Hr, Wr, AXES, SCALE_FACTOR, THETA)).to(dev))
+        dr = kd_fa.make_desc(qr, kr, vr, None, orr, 1.0 / D ** 0.5)
+        wsr = torch.empty(kr.numel(), dtype=bf, device=dev)
+        flr = 4.0 * B * HEADS * Lr * Lr * D
+        for tag, wsx in (("ws", wsr), ("staged", None)):
+            msr = time_launches(torch, lambda: kd_fa.run_desc(dr, ropr, stream, wsx), 3, 1, stream)
+            sec[f"self_attn_ragged_{Lr}_{tag}_ms"] = round(msr, 4)
+            sec[f"self_attn_ragged_{Lr}_{tag}_tflops"] = round(flr / (msr * 1e-3) / 1e12, 2)
+        del qr, kr, vr, orr, wsr
         # text cross-attention: Q 31,744 x K/V 256, batch 2, padding mask 120 / 40 valid keys
         k2 = rand(torch, (B, HEADS, 256, D), 1002, dev, bf)
         v2 = rand(torch, (B, HEADS, 256, D), 2002, dev, bf)

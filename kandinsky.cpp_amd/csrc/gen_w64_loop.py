@@ -570,8 +570,11 @@ class Gen:
                     a = A_O + 64 * qb + 16 * dblk + 4 * g
                     e(Ins(f"ds_write_b128 %[ord], {arng(a, 4)} offset:{((qb * 4 + dblk) * 4 + g) * 1024}", "lds_wr",
                           aset(a, 4), ()))
+        # the half-row sums, and the running maxima for a partial last tile
+        # that the kernel finishes after the loop
         for qb in range(2):
             e(Ins(f"ds_write_b32 %[lrd], {vr(LH[qb])} offset:{256 * qb}", "lds_wr", {vr(LH[qb])}, ()))
+            e(Ins(f"ds_write_b32 %[lrd], {vr(M[qb])} offset:{2048 + 256 * qb}", "lds_wr", {vr(M[qb])}, ()))
         tr.raw("s_waitcnt lgkmcnt(0)")
         tr.raw("s_branch .Lw64_end_%=")
         lines = tr.out

@@ -160,11 +160,12 @@ size_t rope_ws_bytes(const kd_fa_desc *d) {
 // the attention kernel on every K tile it loads.
 
 // The 64-rows-per-wave kernel takes the unmasked calls whose K streams from
-// memory as stored (no transform on load) and whose keys fill whole 64-key
-// tiles; its buffer-resource offsets are 32-bit.  KD_FA_ROUTE_NO_W64 routes
-// every call to the 32-row kernel (for comparisons).
+// memory as stored (no transform on load) and that have at least one whole
+// 64-key tile (a partial last tile is finished after its key loop); its
+// buffer-resource offsets are 32-bit.  KD_FA_ROUTE_NO_W64 routes every call
+// to the 32-row kernel (for comparisons).
 static bool use_w64(const kdfa::Args &a, bool k_on_load, int route) {
-    if ((route & KD_FA_ROUTE_NO_W64) || a.m || k_on_load || a.Lk < 64 || a.Lk % 64 != 0) return false;
+    if ((route & KD_FA_ROUTE_NO_W64) || a.m || k_on_load || a.Lk < 64) return false;
     const int64_t lim = (int64_t)1 << 31;
     return (int64_t)(a.Lk - 1) * a.k_nb1 + 256 < lim && (int64_t)(a.Lk - 1) * a.v_nb1 + 256 < lim;
 }
@@ -211,7 +212,7 @@ static void xres_split(kdfa::Args &a) {
 bool staged_ok(const kdfa::Args &a, const kd_fa_desc *d, int route) {
     if ((route & KD_FA_ROUTE_NO_W64) || a.m) return false;
     if (a.rk2 != 1 || a.rk3 != 1 || a.rv2 != 1 || a.rv3 != 1) return false;
-    if (a.Lk < 64 || a.Lk % 64 != 0 || a.Lq < a.Lk) return false;
+    if (a.Lk < 64 || a.Lq < a.Lk) return false;
     const int64_t row = kHeadDim * (int64_t)elem_size(d->dst.type);
     if ((int64_t)d->dst.nb[1] != row) return false;   // the heads of an output row are contiguous
     if ((int64_t)a.H * a.B < 4) return false;
@@ -231,26 +232,72 @@ kdfa::Args head_range(const kdfa::Args &a, int b, int h0, int n) {
     return s;
 }
 
+// Group sizes for run_staged, first to last (the last one rotates K on
+// load).  A launch fills the GPU in rounds of one workgroup per CU (256 on
+// MI355X), one workgroup per 256 query rows and head, and its last round may
+// be partial; the sizes minimise the rounds of all launches (plus a small
+// cost per launch pair; the on-load kernel's rounds count 1.4 times) under
+// the constraints: each group at most `ratio` times the heads of the next
+// (whose output rows hold its transformed K) and within one batch; the last
+// group has 1 to 8 heads.  A dynamic program over (pairs left, size of the
+// next group), O(P^3) per last-group size for P (b, h) pairs, remembered for
+// the last shape of the calling thread.
+std::vector<int> staged_groups(int P, int H, int wg_head, int ratio) {
+    struct Memo {
+        int P = -1, H = -1, wg = -1, ratio = -1;
+        std::vector<int> sizes;
+    };
+    thread_local Memo memo;
+    if (memo.P == P && memo.H == H && memo.wg == wg_head && memo.ratio == ratio) return memo.sizes;
+    auto rounds = [wg_head](int h) { return (double)(((int64_t)h * wg_head + 255) / 256); };
+    constexpr double kLaunch = 0.05, kOnLoad = 1.4;
+    double best_cost = 1e300;
+    std::vector<int> best;
+    std::vector<double> dp((size_t)(P + 1) * (P + 1));
+    std::vector<int> pick((size_t)(P + 1) * (P + 1));
+    for (int n_last = 1; n_last <= 8; ++n_last) {
+        if (n_last > H || n_last >= P) continue;
+        const int E = P - n_last;
+        for (int s = 1; s <= P; ++s) dp[s] = 0.0;   // e = 0
+        for (int e = 1; e <= E; ++e) {
+            const int avail = e - ((e - 1) / H) * H;   // pairs of its batch before e
+            for (int s = 1; s <= P; ++s) {
+                double b = 1e300;
+                int bh = 0;
+                const int top = std::min(ratio * s, avail);
+                for (int h = 1; h <= top; ++h) {
+                    const double c = rounds(h) + kLaunch + dp[(size_t)(e - h) * (P + 1) + h];
+                    if (c < b - 1e-12 || (c < b + 1e-12 && h > bh)) { b = c; bh = h; }
+                }
+                dp[(size_t)e * (P + 1) + s] = b;
+                pick[(size_t)e * (P + 1) + s] = bh;
+            }
+        }
+        const double cost = dp[(size_t)E * (P + 1) + n_last] + kOnLoad * rounds(n_last);
+        if (cost < best_cost) {
+            best_cost = cost;
+            best.clear();
+            for (int e = E, s = n_last; e > 0;) {
+                const int h = pick[(size_t)e * (P + 1) + s];
+                best.push_back(h);
+                e -= h;
+                s = h;
+            }
+            std::reverse(best.begin(), best.end());
+            best.push_back(n_last);
+        }
+    }
+    memo = {P, H, wg_head, ratio, best};
+    return best;
+}
+
 int run_staged(const kdfa::Args &a, int kv_type, hipStream_t hs) {
     const int H = a.H, P = a.H * a.B;
     const int ratio = a.o_type == KD_FA_TYPE_F32 ? 2 : 1;   // transformed K rows per output row
-    const int n_last = std::min(P >= 16 ? 2 : 1, H);
-    // group sizes from the last backwards: each at most `ratio` times the
-    // next, within the batch of its pairs
-    std::vector<int> start;
-    {
-        int end = P - n_last, next = n_last;
-        while (end > 0) {
-            const int b = (end - 1) / H;
-            const int n = std::min(end - b * H, ratio * next);
-            start.push_back(end - n);
-            next = n;
-            end -= n;
-        }
-        std::reverse(start.begin(), start.end());
-        start.push_back(P - n_last);
-        start.push_back(P);
-    }
+    const std::vector<int> sizes = staged_groups(P, H, (a.Lq + 255) / 256, ratio);
+    std::vector<int> start(1, 0);
+    for (int n : sizes) start.push_back(start.back() + n);
+    const int n_last = sizes.back();
     const int n_groups = (int)start.size() - 1;   // the last one rotates K on load
     const int64_t krow = kHeadDim * (int64_t)elem_size(kv_type);
     for (int g = 0; g + 1 < n_groups; ++g) {

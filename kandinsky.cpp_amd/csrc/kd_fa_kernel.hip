@@ -1190,15 +1190,17 @@ void fa_fwd_xres(Args a) {
 // its arithmetic is fa_fwd_d128's step for step, so that both kernels give
 // bitwise identical results.  K and V stream global -> LDS through buffer
 // resources whose record count stops at the last key (a DMA past it reads
-// zeros).  Lk is a positive multiple of 64 (no partial tile).
+// zeros).  The loop runs the whole 64-key tiles (Lk >= 64); a partial last
+// tile is finished after it, in compiled code (see below).
 // LDS: K and V tiles double-buffered (0 .. 64 KiB), the Q fragments handed
 // to the loop (64 .. 128 KiB); after the loop, O (0 .. 128 KiB) and the row
 // sums (128 .. 130 KiB) handed back.
 #include "kd_fa_w64_loop.inc"
 
-constexpr int kW64Lds = 133120;
+constexpr int kW64Lds = 135168;
 constexpr int kW64QOff = 65536;
-constexpr int kW64LOff = 131072;
+constexpr int kW64LOff = 131072;   // half-row sums; running maxima at +2048
+constexpr int kTailV = 32768;      // a partial last tile: K at 0, V here
 
 template <typename T, int RM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -1301,25 +1303,155 @@ void fa_fwd_w64(Args a) {
 #undef KD_W64_OPERANDS
     __syncthreads();
 
-    // O and the half-row sums from LDS -> dst
+    // O, the half-row sums and the running maxima from LDS
+    f32x16 o[2][4];
+    float l_half[2], m_run[2];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
-        f32x16 o[4];
 #pragma unroll
         for (int dblk = 0; dblk < 4; ++dblk)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const f32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) f32x4 *>(
                     lds + wave * 32768 + ((qb * 4 + dblk) * 4 + g) * 1024 + lane * 16);
-                o[dblk][4 * g] = v.x;
-                o[dblk][4 * g + 1] = v.y;
-                o[dblk][4 * g + 2] = v.z;
-                o[dblk][4 * g + 3] = v.w;
+                o[qb][dblk][4 * g] = v.x;
+                o[qb][dblk][4 * g + 1] = v.y;
+                o[qb][dblk][4 * g + 2] = v.z;
+                o[qb][dblk][4 * g + 3] = v.w;
             }
-        const float l_half = *reinterpret_cast<const __attribute__((address_space(3))) float *>(
+        l_half[qb] = *reinterpret_cast<const __attribute__((address_space(3))) float *>(
             lds + kW64LOff + wave * 512 + qb * 256 + lane * 4);
-        store_o_row(a, qt * 256 + wave * 64 + qb * 32 + l32, h, b, hi, o, l_half);
+        m_run[qb] = *reinterpret_cast<const __attribute__((address_space(3))) float *>(
+            lds + kW64LOff + 2048 + wave * 512 + qb * 256 + lane * 4);
     }
+
+    // A partial last tile (Lk not a multiple of 64): the loop has run the
+    // full tiles; the partial one is fa_fwd_d128's tail step, here, with the
+    // same arithmetic -- keys past Lk read key Lk - 1 again and get weight 0
+    // -- so that the result stays bitwise the 32-row kernel's.
+    const int n_full = a.Lk / kBN;
+    if (n_full * kBN < a.Lk) {
+        __syncthreads();   // every wave holds its O: the LDS is free
+        const int Lk = a.Lk;
+        const int t = n_full;
+        // the lane's LDS operand offsets again, from a lane id the compiler
+        // cannot trace back to before the loop (values kept across it would
+        // be spilled: the loop owns nearly every register)
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int tl32 = ln & 31, thi = ln >> 5;
+        uint32_t tkrd[8], tvrd[4];
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) tkrd[ks] = tl32 * 256 + (((2 * ks + thi) ^ (ln & 15)) << 4);
+        {
+            const int vs = (ln & 15) >> 2;
+            const int vc = 2 * ((ln >> 4) & 1) + ((ln & 3) >> 1);
+#pragma unroll
+            for (int dblk = 0; dblk < 4; ++dblk)
+                tvrd[dblk] = kTailV + 2048 * thi + 256 * vs + (((4 * dblk + vc) ^ v_swz(vs)) << 4) + 8 * (ln & 1);
+        }
+        {
+            const char *kt = kbase + (int64_t)t * kBN * a.k_nb1;
+            const char *vt = vbase + (int64_t)t * kBN * a.v_nb1;
+            const int dma_row = ln >> 4, dma_pc = ln & 15;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int r = 4 * (wave + 4 * j) + dma_row;
+                const int kr = t * kBN + k_row_of(r) < Lk ? k_row_of(r) : Lk - 1 - t * kBN;
+                const int vr = t * kBN + r < Lk ? r : Lk - 1 - t * kBN;
+                dma16(kt, (uint32_t)kr * (uint32_t)a.k_nb1 + ((dma_pc ^ (r & 15)) << 4),
+                      lds + (wave + 4 * j) * 1024);
+                dma16(vt, (uint32_t)vr * (uint32_t)a.v_nb1 + ((dma_pc ^ v_swz(r)) << 4),
+                      lds + kTailV + (wave + 4 * j) * 1024);
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        const int key0 = t * kBN;
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            const int q_row = qt * 256 + wave * 64 + qb * 32 + tl32;
+            vec8 qf[8];
+            load_q_frags<T, RM>(a, q_row < a.Lq ? q_row : a.Lq - 1, h, b, thi, qf);
+            // S^T = K Q^T over the tile (k-steps in order, as every kernel)
+            f32x16 s0 = {}, s1 = {};
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+                const vec8 k0 = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(lds + tkrd[ks]);
+                const vec8 k1 = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(
+                    lds + tkrd[ks] + 32 * 256);
+                s0 = E::mfma(k0, qf[ks], s0);
+                s1 = E::mfma(k1, qf[ks], s1);
+            }
+            float m = m_run[qb];
+            float lh = l_half[qb];
+            float p[32];
+            vec8 pb[4];
+            auto weights = [&]() __attribute__((always_inline)) {
+                const float nm = -m;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], c2, nm));
+                    p[16 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], c2, nm));
+                }
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    const int key = key0 + (i >> 4) * 32 + 16 * ((i >> 3) & 1) + 8 * thi + (i & 7);
+                    p[i] = key < Lk ? p[i] : 0.0f;
+                }
+            };
+            // P rounded for PV; the row sum of the F32 weights, each 16-key
+            // step's 8 in order, the steps combined as (s0 + s1) + (s2 + s3)
+            auto pack_sum = [&]() __attribute__((always_inline)) -> float {
+                float part[4];
+#pragma unroll
+                for (int kst = 0; kst < 4; ++kst) {
+                    u32x4 w;
+                    for (int j = 0; j < 4; ++j) w[j] = E::pack2(p[8 * kst + 2 * j], p[8 * kst + 2 * j + 1]);
+                    part[kst] = p[8 * kst] + p[8 * kst + 1];
+                    for (int i = 2; i < 8; ++i) part[kst] += p[8 * kst + i];
+                    pb[kst] = __builtin_bit_cast(vec8, w);
+                }
+                return (part[0] + part[1]) + (part[2] + part[3]);
+            };
+            weights();
+            float sum = pack_sum();
+            if (__builtin_amdgcn_ballot_w64(!(pair_sum(sum) <= E::kSumCap)) != 0) {
+                float q[32];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) { q[i] = s0[i]; q[16 + i] = s1[i]; }
+                const float mx = pair_max(max32(q)) * c2;
+                if (__builtin_amdgcn_ballot_w64(mx > m + kTau) != 0) {
+                    const float m_new = __builtin_fmaxf(m, mx);
+                    const float alpha = m_new == m ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
+                    m = m_new;
+                    lh *= alpha;
+#pragma unroll
+                    for (int dblk = 0; dblk < 4; ++dblk)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) o[qb][dblk][i] *= alpha;
+                }
+                weights();
+                sum = pack_sum();
+            }
+            lh += sum;
+            // O^T += V^T P^T
+#pragma unroll
+            for (int kst = 0; kst < 4; ++kst)
+#pragma unroll
+                for (int dblk = 0; dblk < 4; ++dblk) {
+                    const lds_t *vp = lds + tvrd[dblk] + 4096 * kst;
+                    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(vp));
+                    const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(vp + 1024));
+                    const vec8 va = __builtin_bit_cast(vec8, __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+                    o[qb][dblk] = E::mfma(va, pb[kst], o[qb][dblk]);
+                }
+            l_half[qb] = lh;
+        }
+    }
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+        store_o_row(a, qt * 256 + wave * 64 + qb * 32 + l32, h, b, hi, o[qb], l_half[qb]);
 }
 
 template <typename T>

@@ -12,8 +12,8 @@ subset of the query rows of every wave -- not all of them -- one key beyond
 the first 64-key tile gets a logit 12 to 40 nats above that row's maximum
 over the first tile.  Every output must be finite and within the parity
 gate of the float64 oracle, through each kernel that takes unmasked calls:
-the 64-row kernel (Lk a multiple of 64), the 32-row kernel (routed, and for
-a ragged Lk) and the short-key kernel (Lk <= 256).
+the 64-row kernel (with and without a partial last tile), the 32-row kernel
+routed in its place, and the short-key kernel (Lk <= 256).
 """
 import math
 
@@ -106,13 +106,19 @@ def test_peaks_w64_and_w32(kv, qt):
 
 @pytest.mark.parametrize("Lk", [333, 1000])
 def test_peaks_ragged_keys(Lk):
-    """A ragged Lk: the 32-row kernel with its partial last tile."""
+    """A ragged Lk: the 64-row kernel with its partial last tile finished
+    after the loop, and the 32-row kernel routed in its place -- bitwise
+    equal, finite, within the gate."""
     _need_gpu()
     _announce(f"peaks ragged Lk={Lk} f16")
     B, H, Lq = 2, 2, 257
     q, k, v, planted = spiked(B, H, Lq, Lk, torch.float16, seed=Lk)
-    out = kd_fa.flash_attn_ext(q.to(DEV), k.to(DEV), v.to(DEV))
+    qg, kg, vg = q.to(DEV), k.to(DEV), v.to(DEV)
+    out = kd_fa.flash_attn_ext(qg, kg, vg)
+    with kd_fa.routing(kd_fa.ROUTE_NO_W64):
+        ref = kd_fa.flash_attn_ext(qg, kg, vg)
     torch.cuda.synchronize()
+    assert torch.equal(out, ref)
     _check(out, q, k, v, np.arange(B * H * Lq), H, Lq, f"ragged peaks Lk={Lk}")
 
 

@@ -50,6 +50,9 @@ CASES = [
     (3, 3, (3, 8, 8), torch.bfloat16, torch.float32, torch.bfloat16, "table"),
     (2, 16, (2, 8, 16), torch.float16, torch.float16, torch.float16, "axes"),
     (1, 32, (2, 16, 16), torch.bfloat16, torch.float32, torch.float32, "table"),
+    # token counts that are not multiples of 64 (a partial last key tile)
+    (2, 8, (3, 5, 7), torch.bfloat16, torch.float32, torch.float32, "table"),
+    (1, 6, (5, 9, 16), torch.float16, torch.float16, torch.bfloat16, "axes"),
 ]
 
 

@@ -51,6 +51,14 @@ CASES = [
     (2, 4, 2, 2, 513, 256, torch.bfloat16),
     (1, 2, 2, 1, 1000, 1280, torch.float16),
     (1, 1, 1, 1, 260, 4096, torch.bfloat16),
+    # Lk not a multiple of 64: the whole tiles in the loop, then the partial
+    # tile (1 .. 63 keys) after it; 1 .. many whole tiles
+    (1, 2, 2, 1, 256, 65, torch.bfloat16),
+    (2, 3, 1, 1, 130, 127, torch.float16),
+    (1, 2, 2, 1, 300, 200, torch.bfloat16),
+    (2, 4, 2, 2, 513, 333, torch.float16),
+    (1, 2, 2, 1, 1000, 1337, torch.bfloat16),
+    (1, 1, 1, 1, 77, 4095, torch.float16),
 ]
 
 
@@ -67,13 +75,15 @@ def test_w64_equals_w32(case):
     assert_parity(gather_rows(out, rows, H, Lq), orc.fa_f64(q, k, v, rows=rows), f"w64 {case}")
 
 
+@pytest.mark.parametrize("Lk", [640, 650])
 @pytest.mark.parametrize("scale", [-0.0883883, 0.0, 0.5, 4.0], ids=["neg", "zero", "large", "huge"])
-def test_w64_scales_and_rescale(scale):
+def test_w64_scales_and_rescale(scale, Lk):
     """Keys that grow tile by tile move the running max again and again
-    (the out-of-line rescale of O in the accumulation registers)."""
+    (the out-of-line rescale of O in the accumulation registers; with
+    Lk = 650 the partial last tile's rescale too)."""
     _need_gpu()
-    _announce(f"w64 scale {scale}")
-    B, H, Lq, Lk = 1, 2, 200, 640
+    _announce(f"w64 scale {scale} Lk {Lk}")
+    B, H, Lq = 1, 2, 200
     q, k, v = qkv(B, H, Lq, Lk, torch.bfloat16, seed=31)
     growth = torch.linspace(0.2, 3.0, Lk).view(1, 1, Lk, 1)
     k = (k.float() * growth).to(torch.bfloat16)
@@ -136,3 +146,18 @@ def test_w64_production_shape_sampled():
     assert torch.equal(out, ref)
     rows = sample_rows(B, H, L, 16, seed=62)
     assert_parity(gather_rows(out, rows, H, L), orc.fa_f64(q, k, v, rows=rows), "w64 31744")
+
+
+def test_w64_ragged_production_shape_sampled():
+    """A token count that is not a multiple of 64 at production length:
+    768x432, 121 frames -> latent 31 x 54 x 96, patch (1, 2, 2) -> 31 x 27 x 48
+    = 40,176 tokens (627 whole tiles and 48 keys), one head pair."""
+    _need_gpu()
+    B, H, L = 1, 2, 31 * 27 * 48
+    _announce(f"w64 ragged {L} tokens, 2 heads")
+    q, k, v = qkv(B, H, L, L, torch.bfloat16, seed=63)
+    qg, kg, vg = q.to(DEV), k.to(DEV), v.to(DEV)
+    out, ref = _both(lambda: kd_fa.flash_attn_ext(qg, kg, vg))
+    assert torch.equal(out, ref)
+    rows = sample_rows(B, H, L, 16, seed=64)
+    assert_parity(gather_rows(out, rows, H, L), orc.fa_f64(q, k, v, rows=rows), "w64 ragged 40176")
