@@ -185,6 +185,9 @@ static bool use_xres(const kdfa::Args &a, const kd_fa_desc *d, bool k_on_load, i
 
 // Query ranges per (b, h) for fa_fwd_xres: about one workgroup per CU
 // (256 on MI355X) in all, at least four 32-row blocks (one per wave) each.
+// (Two to four workgroups per CU, which would let the dispatcher balance
+// batches whose masks leave different numbers of live key tiles, measured
+// no faster: each workgroup first loads its K and V.)
 static void xres_split(kdfa::Args &a) {
     const int64_t n_qb = ((int64_t)a.Lq + 31) / 32;
     const int64_t bh = (int64_t)a.H * a.B;

@@ -769,14 +769,16 @@ void fa_fwd_xres(Args a) {
     const int l32 = lane & 31;
     const int hi = lane >> 5;
 
-    // unit (b, range, h), heads fastest; each XCD a contiguous run of units
+    // unit (range, b, h), heads fastest, then batches; each XCD a contiguous
+    // run of units (so that one XCD's ranges mix the batches, whose masks
+    // may leave different numbers of live key tiles)
     const int pid = blockIdx.x;
     const int per = a.n_blocks >> 3;
     const int lid = pid < per * 8 ? (pid & 7) * per + (pid >> 3) : pid;
     const int h = lid % a.H;
     const int rest = lid / a.H;
-    const int range = rest % a.n_qt;
-    const int b = rest / a.n_qt;
+    const int b = rest % a.B;
+    const int range = rest / a.B;
 
     const char *kbase = a.k + (int64_t)(h / a.rk2) * a.k_nb2 + (int64_t)(b / a.rk3) * a.k_nb3;
     const char *vbase = a.v + (int64_t)(h / a.rv2) * a.v_nb2 + (int64_t)(b / a.rv3) * a.v_nb3;
@@ -815,16 +817,34 @@ void fa_fwd_xres(Args a) {
     int qb = range * a.x_blocks + wave;
     if (qb >= qb_end) return;   // no barrier follows
 
-    const float c2 = __builtin_fabsf(a.scale_log2);
-    uint32_t k_rd[8];
+    // Per-lane LDS operand offsets.  The masked kernel computes them from an
+    // opaque copy of the lane index in each tile's products: hoisted out of
+    // the block loop, its 12 offsets were spilled to scratch and reloaded
+    // behind the loop's memory waits (a round trip per block).  The unmasked
+    // kernel has the registers and keeps them.
+    auto k_off = [](int ln, int ks) __attribute__((always_inline)) -> uint32_t {
+        return (uint32_t)((ln & 31) * 256 + (((2 * ks + (ln >> 5)) ^ (ln & 15)) << 4));
+    };
+    auto v_off = [](int ln, int dblk) __attribute__((always_inline)) -> uint32_t {
+        const int sub = (ln & 15) >> 2;
+        const int c_lo = 2 * ((ln >> 4) & 1) + ((ln & 3) >> 1);
+        return (uint32_t)(2048 * (ln >> 5) + 256 * sub + (((4 * dblk + c_lo) ^ v_swz(sub)) << 4) + 8 * (ln & 1));
+    };
+    uint32_t k_rd[8], v_rd[4];
+    if constexpr (!HAS_MASK) {
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) k_rd[ks] = l32 * 256 + (((2 * ks + hi) ^ (lane & 15)) << 4);
-    const int v_sub = (lane & 15) >> 2;
-    const int v_c_lo = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
-    uint32_t v_rd[4];
+        for (int ks = 0; ks < 8; ++ks) k_rd[ks] = k_off(lane, ks);
 #pragma unroll
-    for (int dblk = 0; dblk < 4; ++dblk)
-        v_rd[dblk] = 2048 * hi + 256 * v_sub + (((4 * dblk + v_c_lo) ^ v_swz(v_sub)) << 4) + 8 * (lane & 1);
+        for (int dblk = 0; dblk < 4; ++dblk) v_rd[dblk] = v_off(lane, dblk);
+    }
+    auto k_at = [&](int ln, int ks) __attribute__((always_inline)) -> uint32_t {
+        if constexpr (HAS_MASK) return k_off(ln, ks);
+        return k_rd[ks];
+    };
+    auto v_at = [&](int ln, int dblk) __attribute__((always_inline)) -> uint32_t {
+        if constexpr (HAS_MASK) return v_off(ln, dblk);
+        return v_rd[dblk];
+    };
 
     // ---- operands of a block ----------------------------------------------
     // Q: this lane's 64 elements of its row as stored (Q32: F32, 16 x 16
@@ -832,19 +852,34 @@ void fa_fwd_xres(Args a) {
     // tile as four 16-byte chunks.  The mask rows hold every chunk that
     // starts below Lk; chunks past it re-read the last one and, like the
     // keys of a partial chunk past Lk, count as -inf.
-    const char *const qbase = a.q + (int64_t)h * a.q_nb2 + (int64_t)b * a.q_nb3;
-    const int64_t q_nb1 = a.q_nb1;
-    const char *const mbase = HAS_MASK ? a.m + (int64_t)(h % a.m_ne2) * a.m_nb2 + (int64_t)(b % a.m_ne3) * a.m_nb3
-                                       : nullptr;
-    const int64_t m_nb1 = a.m_nb1;
-    const int Lq = a.Lq;
-    const int o_type = a.o_type;
-    char *const obase = a.o + (int64_t)b * a.o_nb3 + (int64_t)h * a.o_nb1;
-    const int64_t o_nb2 = a.o_nb2;
+    // The block's uniform values (row bases, strides, flags).  The masked
+    // kernel reads them again at the top of every block from the kernel
+    // argument segment, through a pointer made opaque there: kept live across
+    // the block loop they overflowed the scalar registers, were parked in
+    // vector registers and spilled, and the reload waited behind the previous
+    // block's stores.
+    const char *qbase, *mbase;
+    char *obase;
+    int64_t q_nb1, m_nb1, o_nb2;
+    int Lq, o_type;
+    bool qnorm, qneg;
+    float norm_eps, c2;
+    auto load_uniforms = [&](const auto *ap) __attribute__((always_inline)) {
+        qbase = ap->q + (int64_t)h * ap->q_nb2 + (int64_t)b * ap->q_nb3;
+        q_nb1 = ap->q_nb1;
+        mbase = HAS_MASK ? ap->m + (int64_t)(h % ap->m_ne2) * ap->m_nb2 + (int64_t)(b % ap->m_ne3) * ap->m_nb3
+                         : nullptr;
+        m_nb1 = ap->m_nb1;
+        Lq = ap->Lq;
+        o_type = ap->o_type;
+        obase = ap->o + (int64_t)b * ap->o_nb3 + (int64_t)h * ap->o_nb1;
+        o_nb2 = ap->o_nb2;
+        qnorm = ap->qn_w != nullptr;
+        norm_eps = ap->norm_eps;
+        qneg = ap->scale_log2 < 0.0f;
+        c2 = __builtin_fabsf(ap->scale_log2);
+    };
     lds_t *const sO = sV + kXNT * kTileBytes + wave * kXStage;
-    const bool qnorm = a.qn_w != nullptr;
-    const float norm_eps = a.norm_eps;
-    const bool qneg = a.scale_log2 < 0.0f;
     u32x4 qraw[Q32 ? 16 : 8];
     u32x4 mraw[4];
     // hi_b, lk_b: hi and Lk, made opaque once per block so that the
@@ -920,17 +955,19 @@ void fa_fwd_xres(Args a) {
         constexpr int kKPre = HAS_MASK ? 1 : KD_FA_KPRE;
         s0 = (f32x16){};
         s1 = (f32x16){};
+        int ln = lane;
+        if constexpr (HAS_MASK) asm volatile("" : "+v"(ln));
         vec8 ka[8][2];
 #pragma unroll
         for (int ks = 0; ks < kKPre; ++ks) {
-            ka[ks][0] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks]);
-            ka[ks][1] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks] + 32 * 256);
+            ka[ks][0] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_at(ln, ks));
+            ka[ks][1] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_at(ln, ks) + 32 * 256);
         }
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
             if (ks + kKPre < 8) {
-                ka[ks + kKPre][0] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks + kKPre]);
-                ka[ks + kKPre][1] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks + kKPre] + 32 * 256);
+                ka[ks + kKPre][0] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_at(ln, ks + kKPre));
+                ka[ks + kKPre][1] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_at(ln, ks + kKPre) + 32 * 256);
             }
             s0 = E::mfma(ka[ks][0], qf[ks], s0);
             s1 = E::mfma(ka[ks][1], qf[ks], s1);
@@ -962,11 +999,13 @@ void fa_fwd_xres(Args a) {
         return (part[0] + part[1]) + (part[2] + part[3]);
     };
     auto pv = [&](const lds_t *vs_, const vec8 pb[4]) __attribute__((always_inline)) {
+        int ln = lane;
+        if constexpr (HAS_MASK) asm volatile("" : "+v"(ln));
 #pragma unroll
         for (int kst = 0; kst < 4; ++kst) {
 #pragma unroll
             for (int dblk = 0; dblk < 4; ++dblk) {
-                const lds_t *vp = vs_ + v_rd[dblk] + 4096 * kst;
+                const lds_t *vp = vs_ + v_at(ln, dblk) + 4096 * kst;
                 const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(vp));
                 const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(vp + 1024));
                 const vec8 va = __builtin_bit_cast(vec8, __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -1074,7 +1113,14 @@ void fa_fwd_xres(Args a) {
         pv(sV + t * kTileBytes, pb);
     };
 
+    if constexpr (!HAS_MASK) load_uniforms(&a);
     for (; qb < qb_end; qb += kXWaves) {
+        if constexpr (HAS_MASK) {
+            typedef const __attribute__((address_space(4))) Args *args_ptr;
+            args_ptr ap = (args_ptr)__builtin_amdgcn_kernarg_segment_ptr();
+            asm volatile("" : "+s"(ap));
+            load_uniforms(ap);
+        }
         lk_b = Lk;
         hi_b = hi;
         asm volatile("" : "+s"(lk_b), "+v"(hi_b));
