@@ -1495,9 +1495,69 @@ void fa_fwd_w64(Args a) {
             l_half[qb] = lh;
         }
     }
+
+    // O / l -> the rows as whole 128-byte lines (store_o_row_l's arithmetic).
+    // Each wave stages its 64 rows in its own 32 KiB of LDS, row-major with
+    // the 16-byte chunk index XOR the row's low bits (no bank conflicts);
+    // then lane L stores chunk L%32 of row 2j + L/32 (16-bit O: chunk L%16 of
+    // row 4j + L/16), so that each store instruction writes whole lines of
+    // two (four) rows instead of 32-byte pieces of 32 rows, which the memory
+    // wrote as separate partial lines.
+    if (n_full * kBN < a.Lk) __syncthreads();   // every wave has read the tail's K and V
+    {
+        lds_t *const stage = lds + wave * 32768;
+        const bool f32o = a.o_type == KD_FA_TYPE_F32;
+        const bool bfo = a.o_type == KD_FA_TYPE_BF16;
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
-        store_o_row(a, qt * 256 + wave * 64 + qb * 32 + l32, h, b, hi, o[qb], l_half[qb]);
+        for (int qb = 0; qb < 2; ++qb) {
+            const float l_run = pair_sum(l_half[qb]);
+            const float inv = l_run == 0.0f ? 0.0f : 1.0f / l_run;
+            const int r = qb * 32 + l32;
+#pragma unroll
+            for (int dblk = 0; dblk < 4; ++dblk)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x4 v = {o[qb][dblk][4 * g] * inv, o[qb][dblk][4 * g + 1] * inv,
+                                     o[qb][dblk][4 * g + 2] * inv, o[qb][dblk][4 * g + 3] * inv};
+                    if (f32o) {
+                        const int c = dblk * 8 + 2 * g + hi;
+                        *reinterpret_cast<__attribute__((address_space(3))) f32x4 *>(
+                            stage + r * 512 + ((c ^ (r & 31)) << 4)) = v;
+                    } else {
+                        const u32x2 w = bfo ? (u32x2){Elem<__bf16>::pack2(v.x, v.y), Elem<__bf16>::pack2(v.z, v.w)}
+                                            : (u32x2){Elem<_Float16>::pack2(v.x, v.y), Elem<_Float16>::pack2(v.z, v.w)};
+                        const int c = dblk * 4 + g;
+                        *reinterpret_cast<__attribute__((address_space(3))) u32x2 *>(
+                            stage + r * 256 + ((c ^ (r & 15)) << 4) + 8 * hi) = w;
+                    }
+                }
+        }
+        // (LDS operations of a wave complete in order: the reads below see
+        // the writes above)
+        char *const obase = a.o + (int64_t)b * a.o_nb3 + (int64_t)h * a.o_nb1;
+        const int row0 = qt * 256 + wave * 64;
+        const int64_t o_nb2 = a.o_nb2;
+        const int Lq = a.Lq;
+        if (f32o) {
+#pragma unroll 8
+            for (int j = 0; j < 32; ++j) {
+                const int r = 2 * j + (lane >> 5);
+                const int c = lane & 31;
+                const u32x4 w = *reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(
+                    stage + r * 512 + ((c ^ (r & 31)) << 4));
+                if (row0 + r < Lq) *reinterpret_cast<u32x4 *>(obase + (int64_t)(row0 + r) * o_nb2 + c * 16) = w;
+            }
+        } else {
+#pragma unroll 8
+            for (int j = 0; j < 16; ++j) {
+                const int r = 4 * j + (lane >> 4);
+                const int c = lane & 15;
+                const u32x4 w = *reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(
+                    stage + r * 256 + ((c ^ (r & 15)) << 4));
+                if (row0 + r < Lq) *reinterpret_cast<u32x4 *>(obase + (int64_t)(row0 + r) * o_nb2 + c * 16) = w;
+            }
+        }
+    }
 }
 
 template <typename T>
