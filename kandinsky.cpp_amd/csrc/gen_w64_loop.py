@@ -11,7 +11,9 @@ another tile of the same wave.  Per 64-key tile t (step t):
   phase 1   MFMA  S(t+1) = K(t+1) Q^T       32 x 32x32x16, K fragments from LDS
             VALU  softmax of S(t), keys 32-63   (exp2, round to T, row sums)
   check     a row whose weight sum left [0, cap]: exact max, rescale, redo
-            (cap 2^64 for BF16, 2^15 for F16: every rounded weight stays finite)
+            (cap 2^64 for BF16, 2^15 for F16: every rounded weight stays finite);
+            its dependent chain (moves, lane swap, add, compare) spread over
+            the last MFMAs of phase 1, the branch after the last one
   phase 2   MFMA  O^T += V(t)^T P(t)^T       32 x 32x32x16, V^T by ds_read_b64_tr_b16
             VALU  softmax of S(t+1), keys 0-31
 
@@ -31,7 +33,7 @@ instruction there: without them the reader sees the value from before the
 dot2), M0 and the LDS DMA that reads it; and an lgkmcnt wait before the
 first use of every LDS load (at most 15 in flight).
 
-Usage: python3 gen_w64_loop.py [out] [--kpre N] [--vpre N] [--per1 N] [--check-at N]
+Usage: python3 gen_w64_loop.py [out] [--kpre N] [--vpre N] [--per1 N] [--check-at N] [--[no-]check-spread]
 (default out: kd_fa_w64_loop.inc beside it).  The schedule knobs are
 tuning switches for variant builds; the committed loop uses the defaults,
 and the environment is never read.
@@ -76,9 +78,13 @@ KBUF = (0, 16384)
 VBUF = (32768, 49152)
 Q_OFF = 65536
 
-# Phase 1 schedule: VALU instructions after each MFMA, and the MFMA after
-# which the row check runs (the rest of S(t+1) is computed meanwhile)
+# Phase 1 schedule: VALU instructions after each MFMA, and the MFMA before
+# which the row check starts (the rest of S(t+1) is computed meanwhile)
 PER1 = CHECK_AT = None
+# Row check spread over the last MFMAs of phase 1: its dependent chain (moves,
+# lane swap, add, compare) one group per MFMA from MFMA CHECK_AT on, the
+# branch after the last MFMA
+CHECK_SPREAD = False
 
 # Row-sum cap of the lazy running max, as an F32 bit pattern: the weights are
 # rounded to the operand type for PV, so the cap stays inside its range
@@ -86,9 +92,9 @@ SUM_CAP = {"bf16": "0x5f800000",   # 2^64
            "f16": "0x47000000"}    # 2^15 (F16's largest finite value is 65504)
 
 
-def configure(kpre=2, vpre=2, per1=4, check_at=30):
-    global KPRE, VPRE, A_VF, A_LAST, PER1, CHECK_AT
-    KPRE, VPRE, PER1, CHECK_AT = kpre, vpre, per1, check_at
+def configure(kpre=2, vpre=2, per1=4, check_at=29, check_spread=True):
+    global KPRE, VPRE, A_VF, A_LAST, PER1, CHECK_AT, CHECK_SPREAD
+    KPRE, VPRE, PER1, CHECK_AT, CHECK_SPREAD = kpre, vpre, per1, check_at, check_spread
     A_VF = A_KF + 8 * (KPRE + 1)   # V^T fragments: (VPRE + 2) slots x 4
     A_LAST = A_VF + 4 * (VPRE + 2) - 1
     assert A_LAST <= 255
@@ -352,12 +358,15 @@ class Gen:
                 Ins(f"s_cselect_b32 s{base + 2}, 0, s{base + 2}", "salu")]
 
     # ------------------------------------------------------------ pieces
-    def merge(self, tr, seq, valus, extra=(), per=3, tail=None, tail_at=None):
+    def merge(self, tr, seq, valus, extra=(), per=3, tail=None, tail_at=None, spread=(), end=None):
         """MFMAs in order, reads ahead of them, `per` VALU after each,
         `extra` (SALU/VMEM groups) one group after each of the first MFMAs;
-        `tail` (emitting code) after MFMA tail_at - 1 and all of `valus`."""
+        `tail` (emitting code) after MFMA tail_at - 1 and all of `valus`;
+        then the groups of `spread` one after each later MFMA, and `end`
+        (emitting code) after the last MFMA."""
         vi = 0
         extra = list(extra)
+        spread = list(spread)
         tail_at = len(seq) if tail_at is None else tail_at
 
         def finish():
@@ -386,20 +395,39 @@ class Gen:
                     if vi < len(valus):
                         tr.emit(valus[vi])
                         vi += 1
+            elif spread:
+                for x in spread.pop(0):
+                    tr.emit(x)
         if tail_at >= len(seq):
             finish()
+        for grp in spread:
+            for x in grp:
+                tr.emit(x)
+        if end:
+            end(tr)
 
-    def check(self, tr, p, tag):
+    def check_groups(self, p, tag):
         """Row-sum check of both query blocks: one v_permlane32_swap of the
         two blocks' half sums gives block 0's row sums in lanes 0-31 and
-        block 1's in lanes 32-63; the slow paths are out of line."""
-        slow, back = f".Lw64_slow_{tag}_%=", f".Lw64_back_{tag}_%="
+        block 1's in lanes 32-63; the slow paths are out of line.  Returns
+        the groups of the dependent chain and the code of the branch."""
         s0, s1 = PS[0][0], PS[1][0]
-        tr.emit(valu(f"v_mov_b32 {vr(X)}, {vr(s0)}", {vr(s0)}, {vr(X)}))
-        tr.emit(valu(f"v_mov_b32 {vr(Y)}, {vr(s1)}", {vr(s1)}, {vr(Y)}))
-        tr.emit(Ins(f"v_permlane32_swap_b32 {vr(X)}, {vr(Y)}", "perm", {vr(X), vr(Y)}, {vr(X), vr(Y)}))
-        tr.emit(valu(f"v_add_f32 {vr(X)}, {vr(X)}, {vr(Y)}", {vr(X), vr(Y)}, {vr(X)}))
-        tr.emit(valu(f"v_cmp_nge_f32 vcc, {SUM_CAP[self.T]}, {vr(X)}", {vr(X)}, ()))
+        groups = [[valu(f"v_mov_b32 {vr(X)}, {vr(s0)}", {vr(s0)}, {vr(X)}),
+                   valu(f"v_mov_b32 {vr(Y)}, {vr(s1)}", {vr(s1)}, {vr(Y)})],
+                  [Ins(f"v_permlane32_swap_b32 {vr(X)}, {vr(Y)}", "perm", {vr(X), vr(Y)}, {vr(X), vr(Y)})],
+                  [valu(f"v_add_f32 {vr(X)}, {vr(X)}, {vr(Y)}", {vr(X), vr(Y)}, {vr(X)}),
+                   valu(f"v_cmp_nge_f32 vcc, {SUM_CAP[self.T]}, {vr(X)}", {vr(X)}, ())]]
+        return groups, lambda tr: self.check_branch(tr, p, tag)
+
+    def check(self, tr, p, tag):
+        groups, branch = self.check_groups(p, tag)
+        for grp in groups:
+            for x in grp:
+                tr.emit(x)
+        branch(tr)
+
+    def check_branch(self, tr, p, tag):
+        slow, back = f".Lw64_slow_{tag}_%=", f".Lw64_back_{tag}_%="
         tr.emit(Ins(f"s_cbranch_vccnz {slow}", "branch"))
         tr.label(back)
         for qb in range(2):
@@ -483,7 +511,19 @@ class Gen:
                 tr.emit(r)
             dmas = [self.dma("v", VBUF[q], j) for j in range(4)] + [self.advance("v")] + \
                    [self.dma("k", KBUF[p], j) for j in range(4)] + [self.advance("k")]
-            self.merge(tr, seq, self.softmax_half(p, p, 1, (0, 1), True), dmas, PER1, tail, CHECK_AT)
+            if CHECK_SPREAD:
+                groups, branch = self.check_groups(p, tag)
+
+                def head(tr):
+                    for r in vpre:
+                        tr.emit(r)
+                    for x in groups[0]:
+                        tr.emit(x)
+
+                self.merge(tr, seq, self.softmax_half(p, p, 1, (0, 1), True), dmas, PER1, head, CHECK_AT,
+                           groups[1:], branch)
+            else:
+                self.merge(tr, seq, self.softmax_half(p, p, 1, (0, 1), True), dmas, PER1, tail, CHECK_AT)
         else:
             for x in self.softmax_half(p, p, 1, (0, 1), True):
                 tr.emit(x)
@@ -600,8 +640,8 @@ def check_registers(lines):
             assert S_FIRST <= int(m.group(1)) <= S_LAST + 3, ln
 
 
-def main(path=None, kpre=2, vpre=2, per1=4, check_at=30):
-    configure(kpre, vpre, per1, check_at)
+def main(path=None, kpre=2, vpre=2, per1=4, check_at=29, check_spread=True):
+    configure(kpre, vpre, per1, check_at, check_spread)
     here = os.path.dirname(os.path.abspath(__file__))
     path = path or os.path.join(here, "kd_fa_w64_loop.inc")
     out = ["// Generated by gen_w64_loop.py from this directory; do not edit.",
@@ -630,6 +670,7 @@ if __name__ == "__main__":
     ap.add_argument("--kpre", type=int, default=2)
     ap.add_argument("--vpre", type=int, default=2)
     ap.add_argument("--per1", type=int, default=4)
-    ap.add_argument("--check-at", type=int, default=30)
+    ap.add_argument("--check-at", type=int, default=29)
+    ap.add_argument("--check-spread", action=argparse.BooleanOptionalAction, default=True)
     args = ap.parse_args()
-    main(args.out, args.kpre, args.vpre, args.per1, args.check_at)
+    main(args.out, args.kpre, args.vpre, args.per1, args.check_at, args.check_spread)
