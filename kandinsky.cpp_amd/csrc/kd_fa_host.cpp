@@ -59,6 +59,9 @@ int validate(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, b
     if (k.ne[0] != D || v.ne[0] != D || (D != kHeadDim && D != kHeadDimVae)) return KD_FA_ERR_SHAPE;
     const int64_t Lq = q.ne[1], Lk = k.ne[1], H = q.ne[2], B = q.ne[3];
     if (v.ne[1] != Lk) return KD_FA_ERR_SHAPE;
+    // at least one key: the kernels clamp key rows to Lk - 1 (the reference
+    // never builds the node without keys; the caller's fallback takes it)
+    if (Lk == 0) return KD_FA_ERR_SHAPE;
     if (k.ne[2] == 0 || v.ne[2] == 0 || k.ne[3] == 0 || v.ne[3] == 0) return KD_FA_ERR_SHAPE;
     if (H % k.ne[2] || H % v.ne[2] || B % k.ne[3] || B % v.ne[3]) return KD_FA_ERR_SHAPE;
     if (o.ne[0] != v.ne[0] || o.ne[1] != H || o.ne[2] != Lq || o.ne[3] != B) return KD_FA_ERR_SHAPE;
@@ -156,8 +159,9 @@ size_t rope_ws_bytes(const kd_fa_desc *d) {
 
 // K is transformed (normalised and / or rotated) when a norm weight or a
 // RoPE mode asks for it: with ws != nullptr once into ws (contiguous, K's
-// type), after which the attention transforms only Q on load; without, by
-// the attention kernel on every K tile it loads.
+// type), after which the attention transforms only Q on load; without, group
+// by group into output rows of later heads (run_staged) where staged_ok
+// allows, else by the attention kernel on every K tile it loads.
 
 // The 64-rows-per-wave kernel takes the unmasked calls whose K streams from
 // memory as stored (no transform on load) and that have at least one whole

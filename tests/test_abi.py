@@ -205,6 +205,20 @@ def test_run_validates_before_touching_the_device():
     assert kd_fa.lib().kd_fa_run(ctypes.byref(d), None) == kd_fa.ERR_SHAPE
 
 
+def test_no_keys_is_refused():
+    """Lk = 0 is not supported (reason: shape), so that the caller keeps its
+    fallback: the kernels clamp key rows to Lk - 1."""
+    q, k, v, m, dst = _node(Lk=0, mask=True)
+    for mask in (None, m):
+        d = kd_fa.make_desc(q, k, v, mask, dst, 0.1)
+        d.k.data = d.v.data = 16     # zero rows: any aligned non-null pointer, never read
+        if mask is not None:
+            d.mask.data = 16
+        r = ctypes.c_int(0)
+        assert kd_fa.lib().kd_fa_supports(ctypes.byref(d), ctypes.byref(r)) == 0 and r.value == kd_fa.ERR_SHAPE
+        assert kd_fa.lib().kd_fa_run(ctypes.byref(d), None) == kd_fa.ERR_SHAPE
+
+
 def test_empty_query_is_a_no_op():
     q, k, v, m, dst = _node(Lq=0)
     d = kd_fa.make_desc(q, k, v, None, dst, 0.1)
