@@ -1637,20 +1637,19 @@ hipError_t launch(const Args &a, int kv_type, bool k_rope, hipStream_t stream) {
 // lanes, which reduce the row's squares together.
 // ---------------------------------------------------------------------------
 template <typename T, int RM>
-__global__ __launch_bounds__(256) void rope_k_kernel(Args a, char *out, KStrides o, int64_t n_chunks) {
+__global__ __launch_bounds__(256) void rope_k_kernel(Args a, char *out, KStrides o, int n_hb) {
     typedef Elem<T> E;
     const int hk = a.H / a.rk2;   // K heads
-    // n_chunks is a multiple of 16 and so is every lane group's first index:
-    // the 16 lanes of a row enter and leave the loop together
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_chunks;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        const int c = (int)(i & 15);
-        const int64_t row = i >> 4;                  // (b, h, key) flattened, key fastest
-        const int key = (int)(row % a.Lk);
-        const int64_t hb = row / a.Lk;
-        const int h = (int)(hb % hk);
-        const int b = (int)(hb / hk);
-        const int esz = a.k_type == KD_FA_TYPE_F32 ? 4 : 2;
+    // x: 16 keys per workgroup, 16 lanes per key (one 16-byte output chunk
+    // each); y: the (b, h) pairs, uniform per workgroup (no division per
+    // chunk)
+    const int key = (int)blockIdx.x * 16 + (int)(threadIdx.x >> 4);
+    const int c = (int)(threadIdx.x & 15);
+    if (key >= a.Lk) return;
+    const int esz = a.k_type == KD_FA_TYPE_F32 ? 4 : 2;
+    for (int hb = (int)blockIdx.y; hb < n_hb; hb += (int)gridDim.y) {
+        const int h = hb % hk;
+        const int b = hb / hk;
         const char *src = a.k + (int64_t)key * a.k_nb1 + (int64_t)h * a.k_nb2 + (int64_t)b * a.k_nb3 + c * 8 * esz;
         float x[8];
         load8_f32(src, a.k_type, x);
@@ -1669,32 +1668,32 @@ __global__ __launch_bounds__(256) void rope_k_kernel(Args a, char *out, KStrides
 }
 
 template <typename T>
-static void launch_rope_k_t(const Args &a, int grid, char *o, const KStrides &st, int64_t n_chunks,
-                            hipStream_t stream) {
+static void launch_rope_k_t(const Args &a, dim3 grid, char *o, const KStrides &st, int n_hb, hipStream_t stream) {
     switch (a.rope_mode) {
     case KD_FA_ROPE_TABLE:
-        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_TABLE>), dim3(grid), dim3(256), 0, stream, a, o, st, n_chunks);
+        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_TABLE>), grid, dim3(256), 0, stream, a, o, st, n_hb);
         break;
     case KD_FA_ROPE_AXES:
-        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_AXES>), dim3(grid), dim3(256), 0, stream, a, o, st, n_chunks);
+        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_AXES>), grid, dim3(256), 0, stream, a, o, st, n_hb);
         break;
     default:
-        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_NONE>), dim3(grid), dim3(256), 0, stream, a, o, st, n_chunks);
+        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_NONE>), grid, dim3(256), 0, stream, a, o, st, n_hb);
         break;
     }
 }
 
 hipError_t launch_rope_k(const Args &a, int kv_type, int k_heads, int k_batch, void *out, const KStrides &st,
                          hipStream_t stream) {
-    const int64_t n_chunks = (int64_t)a.Lk * k_heads * k_batch * 16;
-    if (n_chunks == 0) return hipSuccess;
-    const int64_t want = (n_chunks + 255) / 256;
-    const int grid = (int)(want < 65536 ? want : 65536);
+    const int64_t n_hb = (int64_t)k_heads * k_batch;
+    if (a.Lk == 0 || n_hb == 0) return hipSuccess;
+    // x: 16 keys per workgroup; y: (b, h) pairs, at most 65,535 (a workgroup
+    // takes every gridDim.y-th pair beyond that)
+    const dim3 grid((unsigned)((a.Lk + 15) / 16), (unsigned)(n_hb < 65535 ? n_hb : 65535));
     char *o = static_cast<char *>(out);
     if (kv_type == KD_FA_TYPE_BF16)
-        launch_rope_k_t<__bf16>(a, grid, o, st, n_chunks, stream);
+        launch_rope_k_t<__bf16>(a, grid, o, st, (int)n_hb, stream);
     else
-        launch_rope_k_t<_Float16>(a, grid, o, st, n_chunks, stream);
+        launch_rope_k_t<_Float16>(a, grid, o, st, (int)n_hb, stream);
     return hipGetLastError();
 }
 
