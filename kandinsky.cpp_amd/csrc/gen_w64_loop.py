@@ -22,8 +22,9 @@ performs, in the same order per row -- the same MFMA accumulation order over
 k-steps and key steps, the same fma / exp2 / rounding, the same row sums
 (the F32 weights of each 16-key step added in order, the steps combined as
 (s0 + s1) + (s2 + s3)), the
-same lazy-max rule decided per 32-row block -- so the two kernels give
-bitwise identical results.
+same lazy-max rule (a row's running max moves only when the row's own tile
+max exceeds it by more than 8) -- so the two kernels give bitwise identical
+results.
 
 The generator also enforces the issue rules of the code it writes: wait
 states between an MFMA result and its non-MFMA readers, VALU results and
@@ -466,12 +467,14 @@ class Gen:
         e(Ins(f"v_permlane32_swap_b32 {vr(X)}, {vr(Y)}", "perm", {vr(X), vr(Y)}, {vr(X), vr(Y)}))
         e(valu(f"v_max_f32 {vr(X)}, {vr(X)}, {vr(Y)}", {vr(X), vr(Y)}, {vr(X)}))
         e(valu(f"v_mul_f32 {vr(X)}, |%[c2]|, {vr(X)}", {vr(X)}, {vr(X)}))
-        # update when some row's max exceeds its running max by more than 8
+        # a row's running max moves when the row's max exceeds it by more
+        # than 8 (per row; the branch skips the rescale when no row moves)
         e(valu(f"v_add_f32 {vr(Y)}, 0x41000000, {vr(M[qb])}", {vr(M[qb])}, {vr(Y)}))
         e(valu(f"v_cmp_gt_f32 vcc, {vr(X)}, {vr(Y)}", {vr(X), vr(Y)}, ()))
         noupd = f".Lw64_noupd_{tag}_%="
         e(Ins(f"s_cbranch_vccz {noupd}", "branch"))
-        e(valu(f"v_max_f32 {vr(Y)}, {vr(M[qb])}, {vr(X)}", {vr(M[qb]), vr(X)}, {vr(Y)}))        # m_new
+        e(valu(f"v_max_f32 {vr(Y)}, {vr(M[qb])}, {vr(X)}", {vr(M[qb]), vr(X)}, {vr(Y)}))
+        e(valu(f"v_cndmask_b32 {vr(Y)}, {vr(M[qb])}, {vr(Y)}, vcc", {vr(M[qb]), vr(Y)}, {vr(Y)}))   # m_new
         e(valu(f"v_sub_f32 {vr(w[2])}, {vr(M[qb])}, {vr(Y)}", {vr(M[qb]), vr(Y)}, {vr(w[2])}))
         e(Ins(f"v_exp_f32 {vr(w[2])}, {vr(w[2])}", "trans", {vr(w[2])}, {vr(w[2])}))
         e(valu(f"v_cmp_neq_f32 vcc, {vr(Y)}, {vr(M[qb])}", {vr(Y), vr(M[qb])}, ()))

@@ -399,10 +399,14 @@ void fa_fwd_d128(Args a) {
         if constexpr (KR ? KD_FA_SCHED_KR : KD_FA_SCHED) sched_qk<kKPre>();
     };
 
-    // rescale O and the sums when the running max moves by more than kTau
+    // the running max of a row moves when the row's tile max exceeds it by
+    // more than kTau (a decision per row, so that every row's result depends
+    // on its own scores only: the ballot just skips the rescale when no row
+    // of the wave moves); O and the sums of a moved row are rescaled
     auto update_max = [&](float mx) __attribute__((always_inline)) {
-        if (__builtin_amdgcn_ballot_w64(mx > m_run + kTau) != 0) {
-            const float m_new = __builtin_fmaxf(m_run, mx);
+        const bool up = mx > m_run + kTau;
+        if (__builtin_amdgcn_ballot_w64(up) != 0) {
+            const float m_new = up ? __builtin_fmaxf(m_run, mx) : m_run;
             const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
             m_run = m_new;
             l_half *= alpha;
@@ -974,9 +978,10 @@ void fa_fwd_xres(Args a) {
         }
         if constexpr (KD_FA_SCHED) sched_qk<kKPre>();
     };
-    auto update_max = [&](float mx) __attribute__((always_inline)) {
-        if (__builtin_amdgcn_ballot_w64(mx > m_run + kTau) != 0) {
-            const float m_new = __builtin_fmaxf(m_run, mx);
+    auto update_max = [&](float mx) __attribute__((always_inline)) {   // fa_fwd_d128's rule, per row
+        const bool up = mx > m_run + kTau;
+        if (__builtin_amdgcn_ballot_w64(up) != 0) {
+            const float m_new = up ? __builtin_fmaxf(m_run, mx) : m_run;
             const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
             m_run = m_new;
             l_half *= alpha;
@@ -1467,8 +1472,9 @@ void fa_fwd_w64(Args a) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) { q[i] = s0[i]; q[16 + i] = s1[i]; }
                 const float mx = pair_max(max32(q)) * c2;
-                if (__builtin_amdgcn_ballot_w64(mx > m + kTau) != 0) {
-                    const float m_new = __builtin_fmaxf(m, mx);
+                const bool up = mx > m + kTau;   // per row, as update_max
+                if (__builtin_amdgcn_ballot_w64(up) != 0) {
+                    const float m_new = up ? __builtin_fmaxf(m, mx) : m;
                     const float alpha = m_new == m ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
                     m = m_new;
                     lh *= alpha;
