@@ -444,9 +444,9 @@ class Gen:
         self.slow.append(blk)
 
     def slow_block(self, p, qb, tag):
-        """Exact row max of S[p][qb], O / sum rescale when it moved by more
-        than 8, all 32 weights again (update_max and the slow path of
-        soft_pv in kd_fa_kernel.hip)."""
+        """Exact row max of S[p][qb]; the rows whose own weight sum failed
+        the check move to it, with O and the sums rescaled; all 32 weights
+        again (move_max and the slow path of soft_pv in kd_fa_kernel.hip)."""
         tr = Tracker()
         sb = S_BASE[p] + 32 * qb
         w = [W_BASE + i for i in range(7)]
@@ -467,12 +467,13 @@ class Gen:
         e(Ins(f"v_permlane32_swap_b32 {vr(X)}, {vr(Y)}", "perm", {vr(X), vr(Y)}, {vr(X), vr(Y)}))
         e(valu(f"v_max_f32 {vr(X)}, {vr(X)}, {vr(Y)}", {vr(X), vr(Y)}, {vr(X)}))
         e(valu(f"v_mul_f32 {vr(X)}, |%[c2]|, {vr(X)}", {vr(X)}, {vr(X)}))
-        # a row's running max moves when the row's max exceeds it by more
-        # than 8 (per row; the branch skips the rescale when no row moves)
-        e(valu(f"v_add_f32 {vr(Y)}, 0x41000000, {vr(M[qb])}", {vr(M[qb])}, {vr(Y)}))
-        e(valu(f"v_cmp_gt_f32 vcc, {vr(X)}, {vr(Y)}", {vr(X), vr(Y)}, ()))
-        noupd = f".Lw64_noupd_{tag}_%="
-        e(Ins(f"s_cbranch_vccz {noupd}", "branch"))
+        # a row's running max moves when the row's own weight sum failed
+        # the check: bit r of the block's check mask (row r sits in lanes r
+        # and r + 32), as the lane mask of both halves.  This block runs
+        # only when that mask is not empty.
+        e(Ins(f"s_mov_b32 vcc_lo, s{S_VCC + qb}", "salu"))
+        e(Ins(f"s_mov_b32 vcc_hi, s{S_VCC + qb}", "salu"))
+        e(Ins("s_nop 1", "salu"))
         e(valu(f"v_max_f32 {vr(Y)}, {vr(M[qb])}, {vr(X)}", {vr(M[qb]), vr(X)}, {vr(Y)}))
         e(valu(f"v_cndmask_b32 {vr(Y)}, {vr(M[qb])}, {vr(Y)}, vcc", {vr(M[qb]), vr(Y)}, {vr(Y)}))   # m_new
         e(valu(f"v_sub_f32 {vr(w[2])}, {vr(M[qb])}, {vr(Y)}", {vr(M[qb]), vr(Y)}, {vr(w[2])}))
@@ -491,7 +492,6 @@ class Gen:
             for i in range(4):
                 a = f"a{A_O + 64 * qb + c + i}"
                 e(Ins(f"v_accvgpr_write_b32 {a}, {vr(tmp[i])}", "accw", {vr(tmp[i])}, {a}))
-        tr.label(noupd)
         for x in self.softmax_half(p, p, 0, (qb,), True) + self.softmax_half(p, p, 1, (qb,), True):
             e(x)
         return tr.out

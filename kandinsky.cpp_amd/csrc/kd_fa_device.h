@@ -34,11 +34,15 @@ typedef __attribute__((address_space(3))) char lds_t;
 
 constexpr int kD = 128;          // head dim (Dk = Dv)
 constexpr float kLog2e = 1.4426950408889634f;
-// Lazy rescale: the running max moves only when a row max exceeds it by
-// more than kTau (log2 units), so P <= 2^kTau before normalisation.
+// Lazy rescale, masked path: a row's running max moves only when the row's
+// tile max exceeds it by more than kTau (log2 units), so P <= 2^kTau before
+// normalisation.
 constexpr float kTau = 8.0f;
 // Unmasked path: a row's weights of one 64-key tile, taken against the
-// running max, may sum up to Elem<T>::kSumCap before the max is refreshed.
+// running max, may sum up to Elem<T>::kSumCap; the row's max moves (to the
+// exact max) only when its own sum leaves [0, kSumCap].  Both rules are
+// decided per row, so a row's result depends on its own scores only, not on
+// which rows share its wave.
 // Every weight is at most that sum and is rounded to T for the PV product,
 // so the cap must stay inside T's finite range: BF16 2^64 (no F32 overflow
 // of O for any |V| < 2^40 and Lk < 2^20); F16 2^15, below its largest

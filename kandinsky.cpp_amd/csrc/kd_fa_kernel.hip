@@ -399,12 +399,13 @@ void fa_fwd_d128(Args a) {
         if constexpr (KR ? KD_FA_SCHED_KR : KD_FA_SCHED) sched_qk<kKPre>();
     };
 
-    // the running max of a row moves when the row's tile max exceeds it by
-    // more than kTau (a decision per row, so that every row's result depends
-    // on its own scores only: the ballot just skips the rescale when no row
-    // of the wave moves); O and the sums of a moved row are rescaled
-    auto update_max = [&](float mx) __attribute__((always_inline)) {
-        const bool up = mx > m_run + kTau;
+    // the running max of a row moves to mx when `up` (a decision per row, so
+    // that every row's result depends on its own scores only: the ballot
+    // just skips the rescale when no row of the wave moves); O and the sums
+    // of a moved row are rescaled.  Masked rows move when the tile max
+    // exceeds the running max by more than kTau, unmasked rows when their
+    // own weight sum left [0, E::kSumCap].
+    auto move_max = [&](float mx, bool up) __attribute__((always_inline)) {
         if (__builtin_amdgcn_ballot_w64(up) != 0) {
             const float m_new = up ? __builtin_fmaxf(m_run, mx) : m_run;
             const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -416,6 +417,7 @@ void fa_fwd_d128(Args a) {
                 for (int i = 0; i < 16; ++i) o[dblk][i] *= alpha;
         }
     };
+    auto update_max = [&](float mx) __attribute__((always_inline)) { move_max(mx, mx > m_run + kTau); };
 
     // P rounded to the operand type (the PV B operands).  The row sum adds the F32 weights (before rounding): each 16-key step's
     // 8 weights of this lane in order, the four steps combined as
@@ -516,7 +518,7 @@ void fa_fwd_d128(Args a) {
             float q[32];
 #pragma unroll
             for (int i = 0; i < 16; ++i) { q[i] = s0[i]; q[16 + i] = s1[i]; }
-            update_max(pair_max(max32(q)) * c2);
+            move_max(pair_max(max32(q)) * c2, !(pair <= E::kSumCap));
             nm = -m_run;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
@@ -605,7 +607,7 @@ void fa_fwd_d128(Args a) {
                 float q[32];
 #pragma unroll
                 for (int i = 0; i < 16; ++i) { q[i] = c0[i]; q[16 + i] = c1[i]; }
-                update_max(pair_max(max32(q)) * c2);
+                move_max(pair_max(max32(q)) * c2, !(pair <= E::kSumCap));
                 nm = -m_run;
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
@@ -978,8 +980,7 @@ void fa_fwd_xres(Args a) {
         }
         if constexpr (KD_FA_SCHED) sched_qk<kKPre>();
     };
-    auto update_max = [&](float mx) __attribute__((always_inline)) {   // fa_fwd_d128's rule, per row
-        const bool up = mx > m_run + kTau;
+    auto move_max = [&](float mx, bool up) __attribute__((always_inline)) {   // fa_fwd_d128's rules, per row
         if (__builtin_amdgcn_ballot_w64(up) != 0) {
             const float m_new = up ? __builtin_fmaxf(m_run, mx) : m_run;
             const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -991,6 +992,7 @@ void fa_fwd_xres(Args a) {
                 for (int i = 0; i < 16; ++i) o[dblk][i] *= alpha;
         }
     };
+    auto update_max = [&](float mx) __attribute__((always_inline)) { move_max(mx, mx > m_run + kTau); };
     auto pack_sum = [&](const float *p, vec8 pb[4]) -> float {
         float part[4];
 #pragma unroll
@@ -1104,7 +1106,7 @@ void fa_fwd_xres(Args a) {
             float q[32];
 #pragma unroll
             for (int i = 0; i < 16; ++i) { q[i] = s0[i]; q[16 + i] = s1[i]; }
-            update_max(pair_max(max32(q)) * c2);
+            move_max(pair_max(max32(q)) * c2, !(pair <= E::kSumCap));
             nm = -m_run;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
@@ -1467,12 +1469,13 @@ void fa_fwd_w64(Args a) {
             };
             weights();
             float sum = pack_sum();
-            if (__builtin_amdgcn_ballot_w64(!(pair_sum(sum) <= E::kSumCap)) != 0) {
+            const float pair = pair_sum(sum);
+            if (__builtin_amdgcn_ballot_w64(!(pair <= E::kSumCap)) != 0) {
                 float q[32];
 #pragma unroll
                 for (int i = 0; i < 16; ++i) { q[i] = s0[i]; q[16 + i] = s1[i]; }
                 const float mx = pair_max(max32(q)) * c2;
-                const bool up = mx > m + kTau;   // per row, as update_max
+                const bool up = !(pair <= E::kSumCap);   // per row, as move_max
                 if (__builtin_amdgcn_ballot_w64(up) != 0) {
                     const float m_new = up ? __builtin_fmaxf(m, mx) : m;
                     const float alpha = m_new == m ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);

@@ -139,6 +139,31 @@ def test_peaks_short_keys(Lk):
     _check(out, q, k, v, np.arange(B * H * Lq), H, Lq, f"xres peaks Lk={Lk}")
 
 
+@pytest.mark.parametrize("Lk,route", [(77, kd_fa.ROUTE_DEFAULT), (77, kd_fa.ROUTE_NO_XRES),
+                                      (1024, kd_fa.ROUTE_DEFAULT), (1024, kd_fa.ROUTE_NO_W64),
+                                      (333, kd_fa.ROUTE_DEFAULT)],
+                         ids=["short", "short-w32", "w64", "w32", "w64-ragged"])
+def test_rows_independent_of_wave_mates(Lk, route):
+    """A row's result depends on its own scores only: the query rows in a
+    random order give the same rows bitwise.  The planted keys also lift
+    the logits of other rows (their Q correlates with the planted row's), so
+    many rows see a tile max well above their running max without their own
+    weight sum leaving the cap -- the rows whose wave-mates overflow must not
+    move their max because of it."""
+    _need_gpu()
+    _announce(f"row independence Lk={Lk} route={route}")
+    B, H, Lq = 1, 2, 1000
+    q, k, v, _ = spiked(B, H, Lq, Lk, torch.float16, seed=400 + Lk, every=3)
+    perm = torch.from_numpy(np.random.default_rng(Lk).permutation(Lq))
+    qg, kg, vg = q.to(DEV), k.to(DEV), v.to(DEV)
+    with kd_fa.routing(route):
+        out = kd_fa.flash_attn_ext(qg, kg, vg)
+        outp = kd_fa.flash_attn_ext(qg[:, :, perm.to(DEV)].contiguous(), kg, vg)
+    torch.cuda.synchronize()
+    # dst [B, Lq, H, D]: rows along dim 1
+    assert torch.equal(outp, out[:, perm.to(DEV)])
+
+
 def test_peaks_with_rope_workspace_and_16bit_out():
     """The self-attention path with RoPE through the K workspace and an F16
     output: the planted peaks survive the rotation's redistribution of the
