@@ -17,14 +17,21 @@ another tile of the same wave.  Per 64-key tile t (step t):
   phase 2   MFMA  O^T += V(t)^T P(t)^T       32 x 32x32x16, V^T by ds_read_b64_tr_b16
             VALU  softmax of S(t+1), keys 0-31
 
+A partial last tile (Lk not a multiple of 64) runs in the loop like the
+others: its K and V rows past Lk read zeros (the buffer resources end at key
+Lk - 1), and in the step that computes its scores S(n-1) a block taken only
+there sets the scores of keys >= Lk to -inf before any softmax reads them,
+so those keys get weight 0 and never raise a row's max -- as the 32-row
+kernel's tail step gives them.
+
 Every arithmetic step is the one the 32-row kernel (kd_fa_kernel.hip)
 performs, in the same order per row -- the same MFMA accumulation order over
 k-steps and key steps, the same fma / exp2 / rounding, the same row sums
 (the F32 weights of each 16-key step added in order, the steps combined as
 (s0 + s1) + (s2 + s3)), the
-same lazy-max rule (a row's running max moves only when the row's own tile
-max exceeds it by more than 8) -- so the two kernels give bitwise identical
-results.
+same lazy-max rule (a row's running max moves, to its exact tile max, only
+when the row's own weight sum leaves [0, cap]) -- so the two kernels give
+bitwise identical results.
 
 The generator also enforces the issue rules of the code it writes: wait
 states between an MFMA result and its non-MFMA readers, VALU results and
@@ -40,6 +47,7 @@ tuning switches for variant builds; the committed loop uses the defaults,
 and the environment is never read.
 """
 import argparse
+import copy
 import os
 import re
 
@@ -497,9 +505,40 @@ class Gen:
         return tr.out
 
     # -------------------------------------------------------------- step
-    def step(self, tr, p, final, tag):
-        """Step t with parity p: S(t) in S[p], K(t+1) in KBUF[1-p], V(t) in
-        VBUF[p]; P[p] holds the weights of keys 0-31 of tile t."""
+    def mask_tail(self, tr, q, toff, tag):
+        """In the step whose S(t+1) is the partial last tile (t = S_T + toff
+        equals the operand mstep), scores of keys >= Lk in S[q] -> -inf.
+        thr (per lane) = valid keys of the tile - 8 * (lane / 32): register
+        i of key block kb holds key 32 kb + 16 ((i / 8) % 2) + 8 (lane / 32)
+        + i % 8 of the tile.  The block's wait states are counted on a copy
+        of the tracker; the tracker itself goes on as on the path that skips
+        the block (the taken path only adds distance, and its writes are
+        VALU results that only VALU instructions read)."""
+        skip = f".Lw64_nomask_{tag}_%="
+        if toff:
+            tr.raw(f"s_add_u32 s{S_TMP}, s{S_T}, {toff}")
+            tr.raw(f"s_cmp_eq_u32 s{S_TMP}, %[mstep]")
+        else:
+            tr.raw(f"s_cmp_eq_u32 s{S_T}, %[mstep]")
+        tr.raw(f"s_cbranch_scc0 {skip}")
+        tb = copy.deepcopy(tr)
+        n0 = len(tb.out)
+        ninf = vr(W_BASE)      # a slow-path temporary, free here
+        tb.emit(valu(f"v_mov_b32 {ninf}, 0xff800000", (), {ninf}))
+        for kb in range(2):
+            for i in range(16):
+                c = 32 * kb + 16 * ((i >> 3) & 1) + (i & 7)
+                tb.emit(valu(f"v_cmp_lt_i32 vcc, {c}, %[thr]", (), ()))
+                for qb in range(2):
+                    r = vr(S_BASE[q] + 32 * qb + 16 * kb + i)
+                    tb.emit(valu(f"v_cndmask_b32 {r}, {ninf}, {r}, vcc", {r, ninf}, {r}))
+        tr.out.extend(tb.out[n0:])
+        tr.label(skip)
+
+    def step(self, tr, p, final, tag, toff=0):
+        """Step t = S_T + toff with parity p: S(t) in S[p], K(t+1) in
+        KBUF[1-p], V(t) in VBUF[p]; P[p] holds the weights of keys 0-31 of
+        tile t."""
         q = 1 - p
         vpre, vseq = self.pv_stream(VBUF[p], p)
 
@@ -532,6 +571,7 @@ class Gen:
                 tr.emit(x)
             tail(tr)
         if not final:
+            self.mask_tail(tr, q, toff, tag)
             self.merge(tr, vseq, self.softmax_half(q, q, 0, (0, 1), True))
             tr.raw("s_waitcnt vmcnt(0)")
             tr.raw("s_barrier")
@@ -587,15 +627,15 @@ class Gen:
         tr.raw(f"s_add_u32 s{S_TMP}, s{S_T}, 2")
         tr.raw(f"s_cmp_lt_u32 s{S_TMP}, %[n]")
         tr.raw(".Lw64_tail_%=".join(["s_cbranch_scc0 ", ""]))
-        self.step(tr, 0, False, "a")
-        self.step(tr, 1, False, "b")
+        self.step(tr, 0, False, "a", 0)
+        self.step(tr, 1, False, "b", 1)
         tr.raw(f"s_add_u32 s{S_T}, s{S_T}, 2")
         tr.raw("s_branch .Lw64_loop_%=")
         tr.label(".Lw64_tail_%=")
         tr.raw(f"s_add_u32 s{S_TMP}, s{S_T}, 1")
         tr.raw(f"s_cmp_lt_u32 s{S_TMP}, %[n]")
         tr.raw("s_cbranch_scc0 .Lw64_last0_%=")
-        self.step(tr, 0, False, "c")
+        self.step(tr, 0, False, "c", 0)
         self.step(tr, 1, True, "d")
         tr.raw("s_branch .Lw64_done_%=")
         tr.label(".Lw64_last0_%=")
@@ -613,11 +653,9 @@ class Gen:
                     a = A_O + 64 * qb + 16 * dblk + 4 * g
                     e(Ins(f"ds_write_b128 %[ord], {arng(a, 4)} offset:{((qb * 4 + dblk) * 4 + g) * 1024}", "lds_wr",
                           aset(a, 4), ()))
-        # the half-row sums, and the running maxima for a partial last tile
-        # that the kernel finishes after the loop
+        # the half-row sums
         for qb in range(2):
             e(Ins(f"ds_write_b32 %[lrd], {vr(LH[qb])} offset:{256 * qb}", "lds_wr", {vr(LH[qb])}, ()))
-            e(Ins(f"ds_write_b32 %[lrd], {vr(M[qb])} offset:{2048 + 256 * qb}", "lds_wr", {vr(M[qb])}, ()))
         tr.raw("s_waitcnt lgkmcnt(0)")
         tr.raw("s_branch .Lw64_end_%=")
         lines = tr.out

@@ -163,13 +163,19 @@ size_t rope_ws_bytes(const kd_fa_desc *d) {
 // by group into output rows of later heads (run_staged) where staged_ok
 // allows, else by the attention kernel on every K tile it loads.
 
+// The 64-row kernel runs a partial last tile in its key loop with the
+// scores of the keys past Lk set to -inf, which gives them weight 0 only
+// while the scale is not 0 (-inf * 0 is NaN): with scale 0 and a partial
+// tile the call goes to the 32-row kernel, which zeroes those weights after
+// the exponent.
+static bool w64_tail_ok(const kdfa::Args &a) { return a.Lk % 64 == 0 || a.scale_log2 != 0.0f; }
+
 // The 64-rows-per-wave kernel takes the unmasked calls whose K streams from
 // memory as stored (no transform on load) and that have at least one whole
-// 64-key tile (a partial last tile is finished after its key loop); its
-// buffer-resource offsets are 32-bit.  KD_FA_ROUTE_NO_W64 routes every call
-// to the 32-row kernel (for comparisons).
+// 64-key tile; its buffer-resource offsets are 32-bit.  KD_FA_ROUTE_NO_W64
+// routes every call to the 32-row kernel (for comparisons).
 static bool use_w64(const kdfa::Args &a, bool k_on_load, int route) {
-    if ((route & KD_FA_ROUTE_NO_W64) || a.m || k_on_load || a.Lk < 64) return false;
+    if ((route & KD_FA_ROUTE_NO_W64) || a.m || k_on_load || a.Lk < 64 || !w64_tail_ok(a)) return false;
     const int64_t lim = (int64_t)1 << 31;
     return (int64_t)(a.Lk - 1) * a.k_nb1 + 256 < lim && (int64_t)(a.Lk - 1) * a.v_nb1 + 256 < lim;
 }
@@ -219,7 +225,7 @@ static void xres_split(kdfa::Args &a) {
 bool staged_ok(const kdfa::Args &a, const kd_fa_desc *d, int route) {
     if ((route & KD_FA_ROUTE_NO_W64) || a.m) return false;
     if (a.rk2 != 1 || a.rk3 != 1 || a.rv2 != 1 || a.rv3 != 1) return false;
-    if (a.Lk < 64 || a.Lq < a.Lk) return false;
+    if (a.Lk < 64 || a.Lq < a.Lk || !w64_tail_ok(a)) return false;
     const int64_t row = kHeadDim * (int64_t)elem_size(d->dst.type);
     if ((int64_t)d->dst.nb[1] != row) return false;   // the heads of an output row are contiguous
     if ((int64_t)a.H * a.B < 4) return false;

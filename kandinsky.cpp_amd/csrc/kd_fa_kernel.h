@@ -64,9 +64,9 @@ size_t k_workspace_need(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk
 // RoPE mode) when k_rope.
 hipError_t launch(const Args &a, int kv_type, bool k_rope, hipStream_t stream);
 
-// Enqueue the 64-rows-per-wave kernel (no mask, K as stored, Lk >= 64, a
-// partial last key tile finished after the loop; query tiles of 256 rows
-// like the unmasked launch).
+// Enqueue the 64-rows-per-wave kernel (no mask, K as stored, Lk >= 64; a
+// partial last key tile runs in the loop, which needs a scale other than 0;
+// query tiles of 256 rows like the unmasked launch).
 hipError_t launch_w64(const Args &a, int kv_type, hipStream_t stream);
 
 // Enqueue the short-key kernel (K as stored, no RoPE, Lk <= kXresMaxKeys):

@@ -107,6 +107,11 @@ template <int PRE, int VPM> __device__ __forceinline__ void sched_pipe() {
 // this lane holds elements ks*16 + hi*8 .. +7 of each k-step; the lane
 // l ^ 32 the other half.  RMSNorm (qn_w) and RoPE (RM) are applied in F32
 // first; scale < 0 negates Q (exact) so that every score is s * |scale|.
+// Every load of the row is issued before any is used, unconditionally, so
+// the row costs one memory round trip (a branch on Q's type per chunk put
+// each chunk's load and its wait in a block of its own): two 16-byte loads
+// per 8-element chunk, both halves of an F32 chunk or the 16-bit chunk
+// twice, and the values chosen by the type afterwards.
 template <typename T, int RM>
 __device__ __forceinline__ void load_q_frags(const Args &a, int q_ld, int h, int b, int hi,
                                              typename Elem<T>::vec8 qf[8]) {
@@ -114,32 +119,66 @@ __device__ __forceinline__ void load_q_frags(const Args &a, int q_ld, int h, int
     typedef typename E::vec8 vec8;
     constexpr bool ROPE = RM != KD_FA_ROPE_NONE;
     const char *qp = a.q + (int64_t)q_ld * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)b * a.q_nb3;
-    const int esz = a.q_type == KD_FA_TYPE_F32 ? 4 : 2;
+    const bool q32 = a.q_type == KD_FA_TYPE_F32;
+    const bool q_bf16 = a.q_type == KD_FA_TYPE_BF16;
+    u32x4 ra[8], rb[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+        const int d0 = ks * 16 + hi * 8;
+        ra[ks] = ld16(qp + (q32 ? d0 * 4 : d0 * 2));
+        rb[ks] = ld16(qp + (q32 ? d0 * 4 + 16 : d0 * 2));
+    }
+    // the rotation's (cos, sin) pairs and the norm weights, also up front
+    f32x4 rc[ROPE ? 16 : 1];
+    if constexpr (ROPE) {
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            const float *cp = rope_ptr<RM>(a, q_ld, ks * 16 + hi * 8);
+            rc[2 * ks] = *reinterpret_cast<const f32x4 *>(cp);
+            rc[2 * ks + 1] = *reinterpret_cast<const f32x4 *>(cp + 4);
+        }
+    }
+    const bool qnorm = a.qn_w != nullptr;
+    f32x4 wn[16];
+    if (qnorm) {
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            wn[2 * ks] = *reinterpret_cast<const f32x4 *>(a.qn_w + ks * 16 + hi * 8);
+            wn[2 * ks + 1] = *reinterpret_cast<const f32x4 *>(a.qn_w + ks * 16 + hi * 8 + 4);
+        }
+    }
+    auto elems = [&](int ks, float x[8]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t w16 = ra[ks][j];
+            const float lo16 = q_bf16 ? bf16_lo(w16) : f16_lo(w16);
+            const float hi16 = q_bf16 ? bf16_hi(w16) : f16_hi(w16);
+            // F32: elements 0-3 from the first load, 4-7 from the second
+            const float e0 = __uint_as_float(j < 2 ? ra[ks][2 * j] : rb[ks][2 * j - 4]);
+            const float e1 = __uint_as_float(j < 2 ? ra[ks][2 * j + 1] : rb[ks][2 * j - 3]);
+            x[2 * j] = q32 ? e0 : lo16;
+            x[2 * j + 1] = q32 ? e1 : hi16;
+        }
+    };
     // RMSNorm of the row (query_norm): this lane holds 64 of its 128
     // elements, the lane l ^ 32 the rest
     float qscale = 1.0f;
-    if (a.qn_w) {
+    if (qnorm) {
         double ss = 0.0;
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
             float x[8];
-            load8_f32(qp + (ks * 16 + hi * 8) * esz, a.q_type, x);
+            elems(ks, x);
             ss += sum_sq8(x);
         }
         qscale = rms_scale(pair_sum_f64(ss), a.norm_eps);
     }
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-        const int d0 = ks * 16 + hi * 8;
         float x[8];
-        load8_f32(qp + d0 * esz, a.q_type, x);
-        if (a.qn_w)
-            rms_apply8(x, qscale, *reinterpret_cast<const f32x4 *>(a.qn_w + d0),
-                       *reinterpret_cast<const f32x4 *>(a.qn_w + d0 + 4));
-        if (ROPE) {
-            const float *cp = rope_ptr<RM>(a, q_ld, d0);
-            rotate8(x, *reinterpret_cast<const f32x4 *>(cp), *reinterpret_cast<const f32x4 *>(cp + 4));
-        }
+        elems(ks, x);
+        if (qnorm) rms_apply8(x, qscale, wn[2 * ks], wn[2 * ks + 1]);
+        if constexpr (ROPE) rotate8(x, rc[2 * ks], rc[2 * ks + 1]);
         u32x4 w;
         for (int j = 0; j < 4; ++j) w[j] = E::pack2(x[2 * j], x[2 * j + 1]);
         if (a.scale_log2 < 0.0f) w ^= (u32x4){0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
@@ -1243,8 +1282,10 @@ void fa_fwd_xres(Args a) {
 // its arithmetic is fa_fwd_d128's step for step, so that both kernels give
 // bitwise identical results.  K and V stream global -> LDS through buffer
 // resources whose record count stops at the last key (a DMA past it reads
-// zeros).  The loop runs the whole 64-key tiles (Lk >= 64); a partial last
-// tile is finished after it, in compiled code (see below).
+// zeros).  The loop runs every 64-key tile (Lk >= 64); in a partial last
+// tile the scores of the keys past Lk (zero rows) are set to -inf before
+// any softmax reads them, which gives them fa_fwd_d128's tail weights (0)
+// and row max (the valid keys').
 // LDS: K and V tiles double-buffered (0 .. 64 KiB), the Q fragments handed
 // to the loop (64 .. 128 KiB); after the loop, O (0 .. 128 KiB) and the row
 // sums (128 .. 130 KiB) handed back.
@@ -1252,8 +1293,7 @@ void fa_fwd_xres(Args a) {
 
 constexpr int kW64Lds = 135168;
 constexpr int kW64QOff = 65536;
-constexpr int kW64LOff = 131072;   // half-row sums; running maxima at +2048
-constexpr int kTailV = 32768;      // a partial last tile: K at 0, V here
+constexpr int kW64LOff = 131072;   // half-row sums
 
 template <typename T, int RM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -1331,7 +1371,13 @@ void fa_fwd_w64(Args a) {
     const uint32_t rw3 = 0x00020000u;
     const uint32_t ktile = __builtin_amdgcn_readfirstlane(64u * (uint32_t)a.k_nb1);
     const uint32_t vtile = __builtin_amdgcn_readfirstlane(64u * (uint32_t)a.v_nb1);
-    const uint32_t n_tiles = __builtin_amdgcn_readfirstlane((uint32_t)(a.Lk / kBN));
+    // every tile, a partial last one included: the loop sets the scores of
+    // its keys past Lk to -inf in step mstep (= n - 2; none when the last
+    // tile is whole), against thr = its valid keys - 8 * (lane / 32)
+    const uint32_t n_tiles = __builtin_amdgcn_readfirstlane((uint32_t)((a.Lk + kBN - 1) / kBN));
+    const int rem = a.Lk - kBN * ((int)n_tiles - 1);
+    const uint32_t mstep = __builtin_amdgcn_readfirstlane(rem < kBN ? n_tiles - 2 : 0xffffffffu);
+    const int thr = rem - 8 * hi;
     const float c2 = __builtin_fabsf(a.scale_log2);
 
     __syncthreads();
@@ -1343,7 +1389,7 @@ void fa_fwd_w64(Args a) {
         [vdma2] "v"(vdma[2]), [vdma3] "v"(vdma[3]), [qrd] "v"(qrd), [ord] "v"(ord), [lrd] "v"(lrd),        \
         [kw0] "s"(kw0), [kw1] "s"(kw1), [kw2] "s"(kw2), [kw3] "s"(rw3), [vw0] "s"(vw0), [vw1] "s"(vw1),    \
         [vw2] "s"(vw2), [vw3] "s"(rw3), [ktile] "s"(ktile), [vtile] "s"(vtile), [n] "s"(n_tiles),          \
-        [c2] "s"(c2), [dmab] "s"(dmab)
+        [c2] "s"(c2), [dmab] "s"(dmab), [mstep] "s"(mstep), [thr] "v"(thr)
 // (m0 is in the clobber list for the reader; the compiler reserves it and
 // uses it nowhere in this kernel)
 #pragma clang diagnostic push
@@ -1356,9 +1402,9 @@ void fa_fwd_w64(Args a) {
 #undef KD_W64_OPERANDS
     __syncthreads();
 
-    // O, the half-row sums and the running maxima from LDS
+    // O and the half-row sums from LDS
     f32x16 o[2][4];
-    float l_half[2], m_run[2];
+    float l_half[2];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
 #pragma unroll
@@ -1374,135 +1420,6 @@ void fa_fwd_w64(Args a) {
             }
         l_half[qb] = *reinterpret_cast<const __attribute__((address_space(3))) float *>(
             lds + kW64LOff + wave * 512 + qb * 256 + lane * 4);
-        m_run[qb] = *reinterpret_cast<const __attribute__((address_space(3))) float *>(
-            lds + kW64LOff + 2048 + wave * 512 + qb * 256 + lane * 4);
-    }
-
-    // A partial last tile (Lk not a multiple of 64): the loop has run the
-    // full tiles; the partial one is fa_fwd_d128's tail step, here, with the
-    // same arithmetic -- keys past Lk read key Lk - 1 again and get weight 0
-    // -- so that the result stays bitwise the 32-row kernel's.
-    const int n_full = a.Lk / kBN;
-    if (n_full * kBN < a.Lk) {
-        __syncthreads();   // every wave holds its O: the LDS is free
-        const int Lk = a.Lk;
-        const int t = n_full;
-        // the lane's LDS operand offsets again, from a lane id the compiler
-        // cannot trace back to before the loop (values kept across it would
-        // be spilled: the loop owns nearly every register)
-        int ln = lane;
-        asm volatile("" : "+v"(ln));
-        const int tl32 = ln & 31, thi = ln >> 5;
-        uint32_t tkrd[8], tvrd[4];
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) tkrd[ks] = tl32 * 256 + (((2 * ks + thi) ^ (ln & 15)) << 4);
-        {
-            const int vs = (ln & 15) >> 2;
-            const int vc = 2 * ((ln >> 4) & 1) + ((ln & 3) >> 1);
-#pragma unroll
-            for (int dblk = 0; dblk < 4; ++dblk)
-                tvrd[dblk] = kTailV + 2048 * thi + 256 * vs + (((4 * dblk + vc) ^ v_swz(vs)) << 4) + 8 * (ln & 1);
-        }
-        {
-            const char *kt = kbase + (int64_t)t * kBN * a.k_nb1;
-            const char *vt = vbase + (int64_t)t * kBN * a.v_nb1;
-            const int dma_row = ln >> 4, dma_pc = ln & 15;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int r = 4 * (wave + 4 * j) + dma_row;
-                const int kr = t * kBN + k_row_of(r) < Lk ? k_row_of(r) : Lk - 1 - t * kBN;
-                const int vr = t * kBN + r < Lk ? r : Lk - 1 - t * kBN;
-                dma16(kt, (uint32_t)kr * (uint32_t)a.k_nb1 + ((dma_pc ^ (r & 15)) << 4),
-                      lds + (wave + 4 * j) * 1024);
-                dma16(vt, (uint32_t)vr * (uint32_t)a.v_nb1 + ((dma_pc ^ v_swz(r)) << 4),
-                      lds + kTailV + (wave + 4 * j) * 1024);
-            }
-        }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        const int key0 = t * kBN;
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-            const int q_row = qt * 256 + wave * 64 + qb * 32 + tl32;
-            vec8 qf[8];
-            load_q_frags<T, RM>(a, q_row < a.Lq ? q_row : a.Lq - 1, h, b, thi, qf);
-            // S^T = K Q^T over the tile (k-steps in order, as every kernel)
-            f32x16 s0 = {}, s1 = {};
-#pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
-                const vec8 k0 = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(lds + tkrd[ks]);
-                const vec8 k1 = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(
-                    lds + tkrd[ks] + 32 * 256);
-                s0 = E::mfma(k0, qf[ks], s0);
-                s1 = E::mfma(k1, qf[ks], s1);
-            }
-            float m = m_run[qb];
-            float lh = l_half[qb];
-            float p[32];
-            vec8 pb[4];
-            auto weights = [&]() __attribute__((always_inline)) {
-                const float nm = -m;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], c2, nm));
-                    p[16 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], c2, nm));
-                }
-#pragma unroll
-                for (int i = 0; i < 32; ++i) {
-                    const int key = key0 + (i >> 4) * 32 + 16 * ((i >> 3) & 1) + 8 * thi + (i & 7);
-                    p[i] = key < Lk ? p[i] : 0.0f;
-                }
-            };
-            // P rounded for PV; the row sum of the F32 weights, each 16-key
-            // step's 8 in order, the steps combined as (s0 + s1) + (s2 + s3)
-            auto pack_sum = [&]() __attribute__((always_inline)) -> float {
-                float part[4];
-#pragma unroll
-                for (int kst = 0; kst < 4; ++kst) {
-                    u32x4 w;
-                    for (int j = 0; j < 4; ++j) w[j] = E::pack2(p[8 * kst + 2 * j], p[8 * kst + 2 * j + 1]);
-                    part[kst] = p[8 * kst] + p[8 * kst + 1];
-                    for (int i = 2; i < 8; ++i) part[kst] += p[8 * kst + i];
-                    pb[kst] = __builtin_bit_cast(vec8, w);
-                }
-                return (part[0] + part[1]) + (part[2] + part[3]);
-            };
-            weights();
-            float sum = pack_sum();
-            const float pair = pair_sum(sum);
-            if (__builtin_amdgcn_ballot_w64(!(pair <= E::kSumCap)) != 0) {
-                float q[32];
-#pragma unroll
-                for (int i = 0; i < 16; ++i) { q[i] = s0[i]; q[16 + i] = s1[i]; }
-                const float mx = pair_max(max32(q)) * c2;
-                const bool up = !(pair <= E::kSumCap);   // per row, as move_max
-                if (__builtin_amdgcn_ballot_w64(up) != 0) {
-                    const float m_new = up ? __builtin_fmaxf(m, mx) : m;
-                    const float alpha = m_new == m ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
-                    m = m_new;
-                    lh *= alpha;
-#pragma unroll
-                    for (int dblk = 0; dblk < 4; ++dblk)
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) o[qb][dblk][i] *= alpha;
-                }
-                weights();
-                sum = pack_sum();
-            }
-            lh += sum;
-            // O^T += V^T P^T
-#pragma unroll
-            for (int kst = 0; kst < 4; ++kst)
-#pragma unroll
-                for (int dblk = 0; dblk < 4; ++dblk) {
-                    const lds_t *vp = lds + tvrd[dblk] + 4096 * kst;
-                    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(vp));
-                    const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(vp + 1024));
-                    const vec8 va = __builtin_bit_cast(vec8, __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
-                    o[qb][dblk] = E::mfma(va, pb[kst], o[qb][dblk]);
-                }
-            l_half[qb] = lh;
-        }
     }
 
     // O / l -> the rows as whole 128-byte lines (store_o_row_l's arithmetic).
@@ -1512,7 +1429,6 @@ void fa_fwd_w64(Args a) {
     // row 4j + L/16), so that each store instruction writes whole lines of
     // two (four) rows instead of 32-byte pieces of 32 rows, which the memory
     // wrote as separate partial lines.
-    if (n_full * kBN < a.Lk) __syncthreads();   // every wave has read the tail's K and V
     {
         lds_t *const stage = lds + wave * 32768;
         const bool f32o = a.o_type == KD_FA_TYPE_F32;
