@@ -171,11 +171,19 @@ size_t rope_ws_bytes(const kd_fa_desc *d) {
 static bool w64_tail_ok(const kdfa::Args &a) { return a.Lk % 64 == 0 || a.scale_log2 != 0.0f; }
 
 // The 64-rows-per-wave kernel takes the unmasked calls whose K streams from
-// memory as stored (no transform on load) and that have at least one whole
-// 64-key tile; its buffer-resource offsets are 32-bit.  KD_FA_ROUTE_NO_W64
-// routes every call to the 32-row kernel (for comparisons).
+// memory as stored (no transform on load) and that have more than
+// kShortKeys keys; its buffer-resource offsets are 32-bit.  (With one
+// workgroup per CU, all CUs load Q, run the few key steps of a short key set
+// and store O in step, while the 32-row kernel's 4-wave workgroups, two per
+// CU, overlap one's memory phases with the other's key loop: cross-attention
+// with Q F32 [128, 31744, 32, 2] and 320 keys 0.62 against 0.72 ms, 512
+// keys 0.78 against 0.85, 896 keys 1.14 against 1.15, 1,024 keys even.)
+// KD_FA_ROUTE_NO_W64 routes every call to the
+// 32-row kernel, KD_FA_ROUTE_W64_SHORT the short key sets too to the 64-row
+// one (for comparisons).
 static bool use_w64(const kdfa::Args &a, bool k_on_load, int route) {
     if ((route & KD_FA_ROUTE_NO_W64) || a.m || k_on_load || a.Lk < 64 || !w64_tail_ok(a)) return false;
+    if (a.Lk <= kdfa::kShortKeys && !(route & KD_FA_ROUTE_W64_SHORT)) return false;
     const int64_t lim = (int64_t)1 << 31;
     return (int64_t)(a.Lk - 1) * a.k_nb1 + 256 < lim && (int64_t)(a.Lk - 1) * a.v_nb1 + 256 < lim;
 }
@@ -324,15 +332,16 @@ int run_staged(const kdfa::Args &a, int kv_type, hipStream_t hs) {
         s.k_nb1 = a.o_nb2;
         s.k_nb2 = krow;
         s.k_nb3 = 0;
-        s.n_qt = (a.Lq + kdfa::block_rows(false, false) - 1) / kdfa::block_rows(false, false);
+        s.n_qt = (a.Lq + kdfa::kW64Rows - 1) / kdfa::kW64Rows;
         s.n_blocks = s.n_qt * n;
         if (kdfa::launch_w64(s, kv_type, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
     }
     const int p0 = start[n_groups - 1];
     kdfa::Args s = head_range(a, p0 / H, p0 % H, n_last);
-    s.n_qt = (a.Lq + kdfa::block_rows(false, true) - 1) / kdfa::block_rows(false, true);
+    const int waves = kdfa::d128_waves(false, true, a.Lk);
+    s.n_qt = (a.Lq + 32 * waves - 1) / (32 * waves);
     s.n_blocks = s.n_qt * n_last;
-    return kdfa::launch(s, kv_type, true, hs) == hipSuccess ? KD_FA_OK : KD_FA_ERR_LAUNCH;
+    return kdfa::launch(s, kv_type, true, waves, hs) == hipSuccess ? KD_FA_OK : KD_FA_ERR_LAUNCH;
 }
 
 int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *ws, size_t ws_bytes,
@@ -407,9 +416,6 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
     }
     bool k_rope = k_xform && !ws;
     if (k_rope && staged_ok(a, d, route)) return run_staged(a, d->v.type, hs);
-    const int rows = kdfa::block_rows(a.m != nullptr, k_rope);
-    a.n_qt = (int32_t)((Lq + rows - 1) / rows);
-    a.n_blocks = (int32_t)(a.n_qt * H * B);
     // a mask row block shared by every head is read once per q-tile when the
     // heads of a q-tile run back to back (K and V of all heads then share the
     // L2 instead, which the short text keys of the cross-attention allow)
@@ -429,9 +435,15 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
     if (use_xres(a, d, k_rope, route)) {
         xres_split(a);
         e = kdfa::launch_xres(a, d->v.type, hs);
+    } else if (use_w64(a, k_rope, route)) {
+        a.n_qt = (int32_t)((Lq + kdfa::kW64Rows - 1) / kdfa::kW64Rows);
+        a.n_blocks = (int32_t)(a.n_qt * H * B);
+        e = kdfa::launch_w64(a, d->v.type, hs);
     } else {
-        e = use_w64(a, k_rope, route) ? kdfa::launch_w64(a, d->v.type, hs)
-                                      : kdfa::launch(a, d->v.type, k_rope, hs);
+        const int waves = kdfa::d128_waves(a.m != nullptr, k_rope, a.Lk);
+        a.n_qt = (int32_t)((Lq + 32 * waves - 1) / (32 * waves));
+        a.n_blocks = (int32_t)(a.n_qt * H * B);
+        e = kdfa::launch(a, d->v.type, k_rope, waves, hs);
     }
     if (e != hipSuccess) return KD_FA_ERR_LAUNCH;
     return KD_FA_OK;

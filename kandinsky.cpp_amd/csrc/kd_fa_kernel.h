@@ -59,10 +59,11 @@ int run_node(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, v
 // *status gets the node's validation status (host-only).
 size_t k_workspace_need(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, int *status);
 
-// Enqueue the forward kernel for K/V element type kv_type on `stream`.
-// Q is normalised (qn_w) and rotated (RoPE mode) on load; K too (kn_w,
-// RoPE mode) when k_rope.
-hipError_t launch(const Args &a, int kv_type, bool k_rope, hipStream_t stream);
+// Enqueue the 32-row kernel for K/V element type kv_type on `stream`, with
+// `waves` waves of 32 query rows per workgroup (d128_waves; a.n_qt and
+// a.n_blocks counted in 32 * waves rows).  Q is normalised (qn_w) and
+// rotated (RoPE mode) on load; K too (kn_w, RoPE mode) when k_rope.
+hipError_t launch(const Args &a, int kv_type, bool k_rope, int waves, hipStream_t stream);
 
 // Enqueue the 64-rows-per-wave kernel (no mask, K as stored, Lk >= 64; a
 // partial last key tile runs in the loop, which needs a scale other than 0;
@@ -91,12 +92,21 @@ struct KStrides {
 hipError_t launch_rope_k(const Args &a, int kv_type, int k_heads, int k_batch, void *out, const KStrides &st,
                          hipStream_t stream);
 
-// Waves per workgroup (32 query rows each): 8 (two waves per SIMD) for the
-// unmasked kernels; 4 for the plain masked one -- the short text
-// cross-attention, where two independent workgroups per CU hide each
-// other's Q load and O store.
-constexpr int waves_per_block(bool masked, bool k_on_load) { return masked && !k_on_load ? 4 : 8; }
-constexpr int block_rows(bool masked, bool k_on_load) { return 32 * waves_per_block(masked, k_on_load); }
+// Waves per workgroup of the 32-row kernel (32 query rows each): 8 (two per
+// SIMD, one workgroup per CU) when it transforms K tiles on load and for
+// unmasked key sets longer than kShortKeys; else 4 -- one wave per SIMD,
+// two independent workgroups per CU, each one's Q load and O store
+// overlapping the other's key loop (the masked text cross-attention, and
+// the unmasked one with a long prompt).
+#ifndef KD_FA_SHORT_KEYS
+#define KD_FA_SHORT_KEYS 896   // tuning switch for variant builds
+#endif
+constexpr int kShortKeys = KD_FA_SHORT_KEYS;
+constexpr int d128_waves(bool masked, bool k_on_load, int Lk) {
+    return k_on_load ? 8 : (masked || Lk <= kShortKeys) ? 4 : 8;
+}
 constexpr int kMinBlockRows = 128;
+// query rows per workgroup of the 64-row kernel
+constexpr int kW64Rows = 256;
 
 }  // namespace kdfa

@@ -191,12 +191,12 @@ __device__ __forceinline__ void store_o_row(const Args &a, int q_row, int h, int
     store_o_row_l(a, q_row, h, b, hi, o, pair_sum(l_half), 0);
 }
 
-template <typename T, bool HAS_MASK, int RM, bool KROPE>
-__global__ __launch_bounds__(64 * waves_per_block(HAS_MASK, KROPE)) __attribute__((amdgpu_waves_per_eu(2)))
+template <typename T, bool HAS_MASK, int RM, bool KROPE, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
 void fa_fwd_d128(Args a) {
     constexpr bool ROPE = RM != KD_FA_ROPE_NONE;   // rotate Q on load
     constexpr bool KR = KROPE;                      // transform K tiles on load
-    constexpr int kWaves = waves_per_block(HAS_MASK, KROPE);
+    constexpr int kWaves = NW;
     constexpr int kThreads = 64 * kWaves;
     constexpr int kBM = 32 * kWaves;                // query rows per workgroup
     constexpr int kRounds = kTileBytes / (kThreads * 16);  // 16-byte DMA rounds per thread per tile
@@ -1526,29 +1526,42 @@ hipError_t launch_w64(const Args &a, int kv_type, hipStream_t stream) {
     return kv_type == KD_FA_TYPE_BF16 ? launch_w64_t<__bf16>(a, stream) : launch_w64_t<_Float16>(a, stream);
 }
 
-template <typename T, bool M, int R, bool KR>
+template <typename T, bool M, int R, bool KR, int NW>
 static hipError_t launch_t(const Args &a, hipStream_t stream) {
-    hipLaunchKernelGGL((fa_fwd_d128<T, M, R, KR>), dim3(a.n_blocks), dim3(64 * waves_per_block(M, KR)), 0, stream, a);
+    hipLaunchKernelGGL((fa_fwd_d128<T, M, R, KR, NW>), dim3(a.n_blocks), dim3(64 * NW), 0, stream, a);
     return hipGetLastError();
 }
 
+// the instances d128_waves chooses: K transformed on load 8 waves, masked 4,
+// unmasked 4 or 8
+template <typename T, bool M, int R>
+static hipError_t launch_w(const Args &a, bool k_rope, int waves, hipStream_t s) {
+    if (k_rope) return waves == 8 ? launch_t<T, M, R, true, 8>(a, s) : hipErrorInvalidValue;
+    if constexpr (M) return waves == 4 ? launch_t<T, M, R, false, 4>(a, s) : hipErrorInvalidValue;
+    else
+        return waves == 4 ? launch_t<T, M, R, false, 4>(a, s)
+                          : waves == 8 ? launch_t<T, M, R, false, 8>(a, s) : hipErrorInvalidValue;
+}
+
 template <typename T, bool M>
-static hipError_t launch_r(const Args &a, bool k_rope, hipStream_t s) {
+static hipError_t launch_r(const Args &a, bool k_rope, int waves, hipStream_t s) {
     switch (a.rope_mode) {
     case KD_FA_ROPE_TABLE:
-        return k_rope ? launch_t<T, M, KD_FA_ROPE_TABLE, true>(a, s) : launch_t<T, M, KD_FA_ROPE_TABLE, false>(a, s);
+        return launch_w<T, M, KD_FA_ROPE_TABLE>(a, k_rope, waves, s);
     case KD_FA_ROPE_AXES:
-        return k_rope ? launch_t<T, M, KD_FA_ROPE_AXES, true>(a, s) : launch_t<T, M, KD_FA_ROPE_AXES, false>(a, s);
+        return launch_w<T, M, KD_FA_ROPE_AXES>(a, k_rope, waves, s);
     default:
-        return k_rope ? launch_t<T, M, KD_FA_ROPE_NONE, true>(a, s) : launch_t<T, M, KD_FA_ROPE_NONE, false>(a, s);
+        return launch_w<T, M, KD_FA_ROPE_NONE>(a, k_rope, waves, s);
     }
 }
 
-hipError_t launch(const Args &a, int kv_type, bool k_rope, hipStream_t stream) {
+hipError_t launch(const Args &a, int kv_type, bool k_rope, int waves, hipStream_t stream) {
     const bool mask = a.m != nullptr;
     if (kv_type == KD_FA_TYPE_BF16)
-        return mask ? launch_r<__bf16, true>(a, k_rope, stream) : launch_r<__bf16, false>(a, k_rope, stream);
-    return mask ? launch_r<_Float16, true>(a, k_rope, stream) : launch_r<_Float16, false>(a, k_rope, stream);
+        return mask ? launch_r<__bf16, true>(a, k_rope, waves, stream)
+                    : launch_r<__bf16, false>(a, k_rope, waves, stream);
+    return mask ? launch_r<_Float16, true>(a, k_rope, waves, stream)
+                : launch_r<_Float16, false>(a, k_rope, waves, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -106,15 +106,16 @@ def test_peaks_w64_and_w32(kv, qt):
 
 @pytest.mark.parametrize("Lk", [333, 1000])
 def test_peaks_ragged_keys(Lk):
-    """A ragged Lk: the 64-row kernel with its partial last tile finished
-    after the loop, and the 32-row kernel routed in its place -- bitwise
-    equal, finite, within the gate."""
+    """A ragged Lk: the 64-row kernel with its partial last tile in the
+    loop, and the 32-row kernel routed in its place -- bitwise equal,
+    finite, within the gate."""
     _need_gpu()
     _announce(f"peaks ragged Lk={Lk} f16")
     B, H, Lq = 2, 2, 257
     q, k, v, planted = spiked(B, H, Lq, Lk, torch.float16, seed=Lk)
     qg, kg, vg = q.to(DEV), k.to(DEV), v.to(DEV)
-    out = kd_fa.flash_attn_ext(qg, kg, vg)
+    with kd_fa.routing(kd_fa.ROUTE_W64_SHORT):
+        out = kd_fa.flash_attn_ext(qg, kg, vg)
     with kd_fa.routing(kd_fa.ROUTE_NO_W64):
         ref = kd_fa.flash_attn_ext(qg, kg, vg)
     torch.cuda.synchronize()
@@ -141,8 +142,8 @@ def test_peaks_short_keys(Lk):
 
 @pytest.mark.parametrize("Lk,route", [(77, kd_fa.ROUTE_DEFAULT), (77, kd_fa.ROUTE_NO_XRES),
                                       (1024, kd_fa.ROUTE_DEFAULT), (1024, kd_fa.ROUTE_NO_W64),
-                                      (333, kd_fa.ROUTE_DEFAULT)],
-                         ids=["short", "short-w32", "w64", "w32", "w64-ragged"])
+                                      (333, kd_fa.ROUTE_DEFAULT), (333, kd_fa.ROUTE_W64_SHORT)],
+                         ids=["short", "short-w32-4w", "w64", "w32-8w", "ragged-w32-4w", "ragged-w64"])
 def test_rows_independent_of_wave_mates(Lk, route):
     """A row's result depends on its own scores only: the query rows in a
     random order give the same rows bitwise.  The planted keys also lift

@@ -1,10 +1,13 @@
 """GPU checks of the 64-rows-per-wave kernel (fa_fwd_w64), which takes the
-unmasked calls whose K is read as stored and whose Lk is a multiple of 64.
+unmasked calls whose K is read as stored and that have more than 896 keys
+(shorter key sets run on the 32-row kernel's 4-wave workgroups unless the
+routing flag KD_FA_ROUTE_W64_SHORT sends them here too).
 
-Each case runs twice through the C ABI: once as routed (fa_fwd_w64) and once
-with the 64-row kernel routed out (kd_fa_set_routing: the 32-row kernel,
-fa_fwd_d128), and the two outputs must
-be bitwise equal -- both kernels perform the same arithmetic per query row.
+Each case runs twice through the C ABI: once on the 64-row kernel
+(kd_fa_set_routing(KD_FA_ROUTE_W64_SHORT)) and once with it routed out
+(KD_FA_ROUTE_NO_W64: the 32-row kernel, fa_fwd_d128), and the two outputs
+must be bitwise equal -- both kernels perform the same arithmetic per query
+row.
 Parity against the float64 oracle completes each case.  The shapes walk the
 loop's control paths: 1 key tile (last step only), 2 (one step + last), 3
 (a step pair + last), 4 (pair + step + last) and many; ragged Lq; GQA and
@@ -34,12 +37,13 @@ def _announce(msg):
 
 
 def _both(fn):
-    """(routed output, 32-row kernel output) of fn()."""
+    """(64-row kernel output, 32-row kernel output) of fn()."""
     with kd_fa.routing(kd_fa.ROUTE_NO_W64):
         ref = fn()
         torch.cuda.synchronize()
-    out = fn()
-    torch.cuda.synchronize()
+    with kd_fa.routing(kd_fa.ROUTE_W64_SHORT):
+        out = fn()
+        torch.cuda.synchronize()
     return out, ref
 
 
@@ -51,8 +55,8 @@ CASES = [
     (2, 4, 2, 2, 513, 256, torch.bfloat16),
     (1, 2, 2, 1, 1000, 1280, torch.float16),
     (1, 1, 1, 1, 260, 4096, torch.bfloat16),
-    # Lk not a multiple of 64: the whole tiles in the loop, then the partial
-    # tile (1 .. 63 keys) after it; 1 .. many whole tiles
+    # Lk not a multiple of 64: the partial last tile (1 .. 63 keys) in the
+    # loop after 1 .. many whole tiles
     (1, 2, 2, 1, 256, 65, torch.bfloat16),
     (2, 3, 1, 1, 130, 127, torch.float16),
     (1, 2, 2, 1, 300, 200, torch.bfloat16),
