@@ -111,8 +111,12 @@ template <int PRE, int VPM> __device__ __forceinline__ void sched_pipe() {
 // the row costs one memory round trip (a branch on Q's type per chunk put
 // each chunk's load and its wait in a block of its own): two 16-byte loads
 // per 8-element chunk, both halves of an F32 chunk or the 16-bit chunk
-// twice, and the values chosen by the type afterwards.
-template <typename T, int RM>
+// twice, and the values chosen by the type afterwards.  TABS: the rotation
+// table's pairs and the norm weights are loaded up front too (64 registers
+// each; where the registers are free), else per chunk.  !QUP: Q too is
+// loaded per chunk (for the kernel that rotates K tiles on load, whose
+// registers are short).
+template <typename T, int RM, bool TABS = false, bool QUP = true>
 __device__ __forceinline__ void load_q_frags(const Args &a, int q_ld, int h, int b, int hi,
                                              typename Elem<T>::vec8 qf[8]) {
     typedef Elem<T> E;
@@ -121,16 +125,18 @@ __device__ __forceinline__ void load_q_frags(const Args &a, int q_ld, int h, int
     const char *qp = a.q + (int64_t)q_ld * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)b * a.q_nb3;
     const bool q32 = a.q_type == KD_FA_TYPE_F32;
     const bool q_bf16 = a.q_type == KD_FA_TYPE_BF16;
-    u32x4 ra[8], rb[8];
+    u32x4 ra[QUP ? 8 : 1], rb[QUP ? 8 : 1];
+    if constexpr (QUP) {
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-        const int d0 = ks * 16 + hi * 8;
-        ra[ks] = ld16(qp + (q32 ? d0 * 4 : d0 * 2));
-        rb[ks] = ld16(qp + (q32 ? d0 * 4 + 16 : d0 * 2));
+        for (int ks = 0; ks < 8; ++ks) {
+            const int d0 = ks * 16 + hi * 8;
+            ra[ks] = ld16(qp + (q32 ? d0 * 4 : d0 * 2));
+            rb[ks] = ld16(qp + (q32 ? d0 * 4 + 16 : d0 * 2));
+        }
     }
-    // the rotation's (cos, sin) pairs and the norm weights, also up front
-    f32x4 rc[ROPE ? 16 : 1];
-    if constexpr (ROPE) {
+    // the rotation's (cos, sin) pairs and the norm weights
+    f32x4 rc[ROPE && TABS ? 16 : 1];
+    if constexpr (ROPE && TABS) {
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
             const float *cp = rope_ptr<RM>(a, q_ld, ks * 16 + hi * 8);
@@ -139,8 +145,8 @@ __device__ __forceinline__ void load_q_frags(const Args &a, int q_ld, int h, int
         }
     }
     const bool qnorm = a.qn_w != nullptr;
-    f32x4 wn[16];
-    if (qnorm) {
+    f32x4 wn[TABS ? 16 : 1];
+    if (TABS && qnorm) {
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
             wn[2 * ks] = *reinterpret_cast<const f32x4 *>(a.qn_w + ks * 16 + hi * 8);
@@ -148,6 +154,10 @@ __device__ __forceinline__ void load_q_frags(const Args &a, int q_ld, int h, int
         }
     }
     auto elems = [&](int ks, float x[8]) __attribute__((always_inline)) {
+        if constexpr (!QUP) {
+            load8_f32(qp + (ks * 16 + hi * 8) * (q32 ? 4 : 2), a.q_type, x);
+            return;
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint32_t w16 = ra[ks][j];
@@ -177,8 +187,22 @@ __device__ __forceinline__ void load_q_frags(const Args &a, int q_ld, int h, int
     for (int ks = 0; ks < 8; ++ks) {
         float x[8];
         elems(ks, x);
-        if (qnorm) rms_apply8(x, qscale, wn[2 * ks], wn[2 * ks + 1]);
-        if constexpr (ROPE) rotate8(x, rc[2 * ks], rc[2 * ks + 1]);
+        const int d0 = ks * 16 + hi * 8;
+        if (qnorm) {
+            if constexpr (TABS)
+                rms_apply8(x, qscale, wn[2 * ks], wn[2 * ks + 1]);
+            else
+                rms_apply8(x, qscale, *reinterpret_cast<const f32x4 *>(a.qn_w + d0),
+                           *reinterpret_cast<const f32x4 *>(a.qn_w + d0 + 4));
+        }
+        if constexpr (ROPE) {
+            if constexpr (TABS) {
+                rotate8(x, rc[2 * ks], rc[2 * ks + 1]);
+            } else {
+                const float *cp = rope_ptr<RM>(a, q_ld, d0);
+                rotate8(x, *reinterpret_cast<const f32x4 *>(cp), *reinterpret_cast<const f32x4 *>(cp + 4));
+            }
+        }
         u32x4 w;
         for (int j = 0; j < 4; ++j) w[j] = E::pack2(x[2 * j], x[2 * j + 1]);
         if (a.scale_log2 < 0.0f) w ^= (u32x4){0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
@@ -248,7 +272,7 @@ void fa_fwd_d128(Args a) {
     const int q_row = qt * kBM + wave * 32 + l32;
     const int q_ld = q_row < a.Lq ? q_row : a.Lq - 1;
     vec8 qf[8];
-    load_q_frags<T, RM>(a, q_ld, h, b, hi, qf);
+    load_q_frags<T, RM, false, !KR>(a, q_ld, h, b, hi, qf);
 
     const uint16_t *mrow = nullptr;
     if (HAS_MASK) {
@@ -1326,7 +1350,7 @@ void fa_fwd_w64(Args a) {
         const int q_row = qt * 256 + wave * 64 + qb * 32 + l32;
         const int q_ld = q_row < a.Lq ? q_row : a.Lq - 1;
         vec8 qf[8];
-        load_q_frags<T, RM>(a, q_ld, h, b, hi, qf);
+        load_q_frags<T, RM, true>(a, q_ld, h, b, hi, qf);
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks)
             *reinterpret_cast<__attribute__((address_space(3))) vec8 *>(
