@@ -48,10 +48,11 @@ def test_caps_agree_and_fit_the_types():
     assert hc["bf16"] == 2.0 ** 64
 
 
-def _lazy_row(s_log2, cap, rnd, tau=8.0):
-    """Per 64-key tile: weights against m; if the sum leaves [0, cap], m
-    moves to the tile max (when it exceeds m by more than tau) and the
-    weights are redone; returns the rounded weights of every tile."""
+def _lazy_row(s_log2, cap, rnd):
+    """Per 64-key tile: weights against m; if the row's own sum leaves
+    [0, cap], m moves to the tile max and the weights are redone (the
+    kernels' rule, decided per row); returns the rounded weights of every
+    tile."""
     m = -np.inf
     out = []
     for t in range(0, len(s_log2), 64):
@@ -60,9 +61,7 @@ def _lazy_row(s_log2, cap, rnd, tau=8.0):
             p = np.exp2(s - m)
             total = p.sum()
         if not total <= cap:
-            mx = s.max()
-            if mx > m + tau:
-                m = max(m, mx)
+            m = max(m, s.max())
             p = np.exp2(s - m)
         with np.errstate(over="ignore"):
             out.append(rnd(p))
