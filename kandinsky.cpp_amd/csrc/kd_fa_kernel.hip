@@ -1598,48 +1598,80 @@ hipError_t launch(const Args &a, int kv_type, bool k_rope, int waves, hipStream_
 // One thread per 8-element chunk; the 16 chunks of a row are 16 consecutive
 // lanes, which reduce the row's squares together.
 // ---------------------------------------------------------------------------
-template <typename T, int RM>
+template <typename T, int RM, int kRopeKPairs>
 __global__ __launch_bounds__(256) void rope_k_kernel(Args a, char *out, KStrides o, int n_hb) {
     typedef Elem<T> E;
     const int hk = a.H / a.rk2;   // K heads
     // x: 16 keys per workgroup, 16 lanes per key (one 16-byte output chunk
-    // each); y: the (b, h) pairs, uniform per workgroup (no division per
-    // chunk)
+    // each); y: groups of kRopeKPairs (b, h) pairs (1 or 4), uniform per workgroup
+    // (no division per chunk).  The chunk's rotation pairs and norm weights
+    // are the same for every (b, h): loaded once.  The group's K chunks are
+    // loaded before any is used, branch-free (both 16-byte halves of an F32
+    // chunk, or the 16-bit chunk twice; past the last pair, the last pair
+    // again, not stored).
     const int key = (int)blockIdx.x * 16 + (int)(threadIdx.x >> 4);
     const int c = (int)(threadIdx.x & 15);
     if (key >= a.Lk) return;
-    const int esz = a.k_type == KD_FA_TYPE_F32 ? 4 : 2;
-    for (int hb = (int)blockIdx.y; hb < n_hb; hb += (int)gridDim.y) {
-        const int h = hb % hk;
-        const int b = hb / hk;
-        const char *src = a.k + (int64_t)key * a.k_nb1 + (int64_t)h * a.k_nb2 + (int64_t)b * a.k_nb3 + c * 8 * esz;
-        float x[8];
-        load8_f32(src, a.k_type, x);
-        u32x4 w;
-        if (a.kn_w)
-            rms_apply8(x, rms_scale(sum16_f64(sum_sq8(x)), a.norm_eps),
-                       *reinterpret_cast<const f32x4 *>(a.kn_w + c * 8),
-                       *reinterpret_cast<const f32x4 *>(a.kn_w + c * 8 + 4));
-        if (RM != KD_FA_ROPE_NONE) {
-            const float *cp = rope_ptr<RM>(a, key, c * 8);
-            rotate8(x, *reinterpret_cast<const f32x4 *>(cp), *reinterpret_cast<const f32x4 *>(cp + 4));
+    const bool k32 = a.k_type == KD_FA_TYPE_F32;
+    const bool kbf = a.k_type == KD_FA_TYPE_BF16;
+    f32x4 cs0 = {}, cs1 = {};
+    if (RM != KD_FA_ROPE_NONE) {
+        const float *cp = rope_ptr<RM>(a, key, c * 8);
+        cs0 = *reinterpret_cast<const f32x4 *>(cp);
+        cs1 = *reinterpret_cast<const f32x4 *>(cp + 4);
+    }
+    const bool knorm = a.kn_w != nullptr;
+    f32x4 wn0 = {}, wn1 = {};
+    if (knorm) {
+        wn0 = *reinterpret_cast<const f32x4 *>(a.kn_w + c * 8);
+        wn1 = *reinterpret_cast<const f32x4 *>(a.kn_w + c * 8 + 4);
+    }
+    const char *const kkey = a.k + (int64_t)key * a.k_nb1 + (k32 ? c * 32 : c * 16);
+    for (int g0 = (int)blockIdx.y * kRopeKPairs; g0 < n_hb; g0 += (int)gridDim.y * kRopeKPairs) {
+        u32x4 ra[kRopeKPairs], rb[kRopeKPairs];
+#pragma unroll
+        for (int i = 0; i < kRopeKPairs; ++i) {
+            const int hb = min(g0 + i, n_hb - 1);
+            const char *src = kkey + (int64_t)(hb % hk) * a.k_nb2 + (int64_t)(hb / hk) * a.k_nb3;
+            ra[i] = ld16(src);
+            rb[i] = ld16(src + (k32 ? 16 : 0));
         }
-        for (int e = 0; e < 4; ++e) w[e] = E::pack2(x[2 * e], x[2 * e + 1]);
-        *reinterpret_cast<u32x4 *>(out + (int64_t)key * o.key + (int64_t)h * o.head + (int64_t)b * o.batch + c * 16) = w;
+#pragma unroll
+        for (int i = 0; i < kRopeKPairs; ++i) {
+            const int hb = g0 + i;
+            if (hb >= n_hb) break;
+            float x[8];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t w16 = ra[i][j];
+                const float lo16 = kbf ? bf16_lo(w16) : f16_lo(w16);
+                const float hi16 = kbf ? bf16_hi(w16) : f16_hi(w16);
+                const float e0 = __uint_as_float(j < 2 ? ra[i][2 * j] : rb[i][2 * j - 4]);
+                const float e1 = __uint_as_float(j < 2 ? ra[i][2 * j + 1] : rb[i][2 * j - 3]);
+                x[2 * j] = k32 ? e0 : lo16;
+                x[2 * j + 1] = k32 ? e1 : hi16;
+            }
+            if (knorm) rms_apply8(x, rms_scale(sum16_f64(sum_sq8(x)), a.norm_eps), wn0, wn1);
+            if (RM != KD_FA_ROPE_NONE) rotate8(x, cs0, cs1);
+            u32x4 w;
+            for (int e = 0; e < 4; ++e) w[e] = E::pack2(x[2 * e], x[2 * e + 1]);
+            *reinterpret_cast<u32x4 *>(out + (int64_t)key * o.key + (int64_t)(hb % hk) * o.head +
+                                       (int64_t)(hb / hk) * o.batch + c * 16) = w;
+        }
     }
 }
 
-template <typename T>
-static void launch_rope_k_t(const Args &a, dim3 grid, char *o, const KStrides &st, int n_hb, hipStream_t stream) {
+template <typename T, int P>
+static void launch_rope_k_p(const Args &a, dim3 grid, char *o, const KStrides &st, int n_hb, hipStream_t stream) {
     switch (a.rope_mode) {
     case KD_FA_ROPE_TABLE:
-        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_TABLE>), grid, dim3(256), 0, stream, a, o, st, n_hb);
+        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_TABLE, P>), grid, dim3(256), 0, stream, a, o, st, n_hb);
         break;
     case KD_FA_ROPE_AXES:
-        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_AXES>), grid, dim3(256), 0, stream, a, o, st, n_hb);
+        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_AXES, P>), grid, dim3(256), 0, stream, a, o, st, n_hb);
         break;
     default:
-        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_NONE>), grid, dim3(256), 0, stream, a, o, st, n_hb);
+        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_NONE, P>), grid, dim3(256), 0, stream, a, o, st, n_hb);
         break;
     }
 }
@@ -1648,14 +1680,24 @@ hipError_t launch_rope_k(const Args &a, int kv_type, int k_heads, int k_batch, v
                          hipStream_t stream) {
     const int64_t n_hb = (int64_t)k_heads * k_batch;
     if (a.Lk == 0 || n_hb == 0) return hipSuccess;
-    // x: 16 keys per workgroup; y: (b, h) pairs, at most 65,535 (a workgroup
-    // takes every gridDim.y-th pair beyond that)
-    const dim3 grid((unsigned)((a.Lk + 15) / 16), (unsigned)(n_hb < 65535 ? n_hb : 65535));
+    // x: 16 keys per workgroup; y: groups of P (b, h) pairs, at most 65,535
+    // (a workgroup takes every gridDim.y-th group beyond that).  P = 4 --
+    // the rotation pairs loaded once for four heads, four loads in flight
+    // per thread -- when that still leaves 2,048 workgroups (62,464 keys x
+    // 32 heads: 0.267 -> 0.200 ms), else 1 (short key sets: more
+    // workgroups rather than more work per thread).
+    const int64_t nx = (a.Lk + 15) / 16;
+    const int P = nx * ((n_hb + 3) / 4) >= 2048 ? 4 : 1;
+    const int64_t n_g = (n_hb + P - 1) / P;
+    const dim3 grid((unsigned)nx, (unsigned)(n_g < 65535 ? n_g : 65535));
     char *o = static_cast<char *>(out);
-    if (kv_type == KD_FA_TYPE_BF16)
-        launch_rope_k_t<__bf16>(a, grid, o, st, (int)n_hb, stream);
-    else
-        launch_rope_k_t<_Float16>(a, grid, o, st, (int)n_hb, stream);
+    if (kv_type == KD_FA_TYPE_BF16) {
+        if (P == 4) launch_rope_k_p<__bf16, 4>(a, grid, o, st, (int)n_hb, stream);
+        else launch_rope_k_p<__bf16, 1>(a, grid, o, st, (int)n_hb, stream);
+    } else {
+        if (P == 4) launch_rope_k_p<_Float16, 4>(a, grid, o, st, (int)n_hb, stream);
+        else launch_rope_k_p<_Float16, 1>(a, grid, o, st, (int)n_hb, stream);
+    }
     return hipGetLastError();
 }
 
