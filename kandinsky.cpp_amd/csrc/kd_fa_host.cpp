@@ -178,9 +178,8 @@ static bool w64_tail_ok(const kdfa::Args &a) { return a.Lk % 64 == 0 || a.scale_
 // CU, overlap one's memory phases with the other's key loop: cross-attention
 // with Q F32 [128, 31744, 32, 2] and 320 keys 0.62 against 0.72 ms, 512
 // keys 0.78 against 0.85, 896 keys 1.14 against 1.15, 1,024 keys even.)
-// KD_FA_ROUTE_NO_W64 routes every call to the
-// 32-row kernel, KD_FA_ROUTE_W64_SHORT the short key sets too to the 64-row
-// one (for comparisons).
+// For comparisons, KD_FA_ROUTE_NO_W64 routes every call to the 32-row
+// kernel and KD_FA_ROUTE_W64_SHORT the short key sets too to this one.
 static bool use_w64(const kdfa::Args &a, bool k_on_load, int route) {
     if ((route & KD_FA_ROUTE_NO_W64) || a.m || k_on_load || a.Lk < 64 || !w64_tail_ok(a)) return false;
     if (a.Lk <= kdfa::kShortKeys && !(route & KD_FA_ROUTE_W64_SHORT)) return false;
