@@ -812,7 +812,7 @@ void fa_fwd_d128(Args a) {
 // give bitwise equal results.
 constexpr int kXNT = 4;      // key tiles held in LDS: Lk <= 256
 constexpr int kXWaves = 8;
-constexpr int kXStage = 2048;   // per wave: 16 rows x 128 bytes of O
+constexpr int kXStage = 4096;   // per wave: 32 rows x 128 bytes of O
 static_assert(kXNT * kBN == kXresMaxKeys, "LDS holds every key");
 
 template <typename T, bool HAS_MASK, bool Q32>
@@ -823,14 +823,13 @@ void fa_fwd_xres(Args a) {
     static_assert(kRounds * kThreads * 16 == kTileBytes, "tile shape");
     typedef Elem<T> E;
     typedef typename E::vec8 vec8;
-    // one LDS object: K tiles at 0, V tiles at 64 KiB, a 2 KiB staging area
-    // per wave for its O rows, the query-norm weights -- so that every K
-    // fragment address is one base register plus an immediate offset (and
-    // every V address one more base)
-    __shared__ __attribute__((aligned(1024))) char lds[2 * kXNT * kTileBytes + kXWaves * kXStage + kD * 4];
+    // one LDS object: K tiles at 0, V tiles at 64 KiB, a 4 KiB staging area
+    // per wave for its O rows (160 KiB in all) -- so that every K fragment
+    // address is one base register plus an immediate offset (and every V
+    // address one more base)
+    __shared__ __attribute__((aligned(1024))) char lds[2 * kXNT * kTileBytes + kXWaves * kXStage];
     lds_t *const sK = LDS_PTR(char, lds);
     lds_t *const sV = sK + kXNT * kTileBytes;
-    float *const lQw = reinterpret_cast<float *>(lds + 2 * kXNT * kTileBytes + kXWaves * kXStage);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -875,8 +874,6 @@ void fa_fwd_xres(Args a) {
                 }
             }
         }
-        if (a.qn_w && tid < kD / 4)
-            reinterpret_cast<f32x4 *>(lQw)[tid] = reinterpret_cast<const f32x4 *>(a.qn_w)[tid];
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -931,6 +928,7 @@ void fa_fwd_xres(Args a) {
     char *obase;
     int64_t q_nb1, m_nb1, o_nb2;
     int Lq, o_type;
+    const float *qn_w;
     bool qnorm, qneg;
     float norm_eps, c2;
     auto load_uniforms = [&](const auto *ap) __attribute__((always_inline)) {
@@ -943,12 +941,20 @@ void fa_fwd_xres(Args a) {
         o_type = ap->o_type;
         obase = ap->o + (int64_t)b * ap->o_nb3 + (int64_t)h * ap->o_nb1;
         o_nb2 = ap->o_nb2;
-        qnorm = ap->qn_w != nullptr;
+        qn_w = ap->qn_w;
+        qnorm = qn_w != nullptr;
         norm_eps = ap->norm_eps;
         qneg = ap->scale_log2 < 0.0f;
         c2 = __builtin_fabsf(ap->scale_log2);
     };
     lds_t *const sO = sV + kXNT * kTileBytes + wave * kXStage;
+    // the query-norm weights, in the first 512 bytes of the wave's staging
+    // area from the start of a block to its epilogue: each block loads its
+    // lane's 8 bytes ahead of the Q rows and leaves them there (read from
+    // memory at their use, they queued behind the Q and mask loads: 4% of
+    // the normalised cross-attention)
+    const __attribute__((address_space(3))) float *const lQw =
+        reinterpret_cast<const __attribute__((address_space(3))) float *>(sO);
     u32x4 qraw[Q32 ? 16 : 8];
     u32x4 mraw[4];
     // hi_b, lk_b: hi and Lk, made opaque once per block so that the
@@ -990,9 +996,10 @@ void fa_fwd_xres(Args a) {
     };
     // load_q_frags' arithmetic (RMSNorm, rounding, sign) on the raw bytes
     vec8 qf[8];
-    auto q_frags = [&]() __attribute__((always_inline)) {
+    auto q_frags = [&](u32x2 qw) __attribute__((always_inline)) {
         float qscale = 1.0f;
         if (qnorm) {
+            *reinterpret_cast<__attribute__((address_space(3))) u32x2 *>(sO + 8 * lane) = qw;
             double ss = 0.0;
 #pragma unroll
             for (int ks = 0; ks < 8; ++ks) {
@@ -1008,8 +1015,8 @@ void fa_fwd_xres(Args a) {
             float x[8];
             q_elems(ks, x);
             if (qnorm)
-                rms_apply8(x, qscale, *reinterpret_cast<const f32x4 *>(lQw + d0),
-                           *reinterpret_cast<const f32x4 *>(lQw + d0 + 4));
+                rms_apply8(x, qscale, *reinterpret_cast<const __attribute__((address_space(3))) f32x4 *>(lQw + d0),
+                           *reinterpret_cast<const __attribute__((address_space(3))) f32x4 *>(lQw + d0 + 4));
             u32x4 w;
             for (int j = 0; j < 4; ++j) w[j] = E::pack2(x[2 * j], x[2 * j + 1]);
             if (qneg) w ^= (u32x4){0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
@@ -1196,13 +1203,19 @@ void fa_fwd_xres(Args a) {
         asm volatile("" : "+s"(lk_b), "+v"(hi_b));
         const int q_row = qb * 32 + l32;
         const int q_ld = q_row < Lq ? q_row : Lq - 1;
+        u32x2 qw = {};
+        if (qnorm) {
+            int ln = lane;   // the offset computed here, not held (and spilled) across the loop
+            asm volatile("" : "+v"(ln));
+            qw = *reinterpret_cast<const u32x2 *>(qn_w + 2 * ln);
+        }
         issue_q(q_ld);
         const uint16_t *mrow = nullptr;
         if (HAS_MASK) {
             mrow = reinterpret_cast<const uint16_t *>(mbase + (int64_t)q_ld * m_nb1);
             issue_m(mrow, 0, mraw);
         }
-        q_frags();
+        q_frags(qw);
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = (f32x16){};
         m_run = -INFINITY;
@@ -1225,68 +1238,61 @@ void fa_fwd_xres(Args a) {
             }
         }
         // O / l -> the rows (store_o_row_l's arithmetic), through the wave's
-        // staging area, 16 rows at a time: the lanes of those rows leave
-        // their 16-byte pieces there (chunk index XOR the row's low bits: no
-        // bank conflicts), then lane L reads chunk L%8 of row 8j + L/8, so
-        // that every store instruction writes eight whole 128-byte lines (one
-        // per row) instead of 32-byte pieces of 32 rows.  F32: one 32-column
-        // block per round; 16-bit: two.  (LDS operations of a wave complete
-        // in order, so a round's reads see its writes and precede the next
-        // round's writes.)
+        // 4 KiB staging area, all 32 rows at a time: each lane leaves its
+        // 16-byte pieces of its row there (chunk index XOR the row's low
+        // bits: no bank conflicts), then lane L reads chunk L%8 of rows
+        // 8j + L/8, so that every store instruction writes eight whole
+        // 128-byte lines (one per row) instead of 32-byte pieces of 32 rows.
+        // F32: one 32-column block per round (4 rounds); 16-bit: two (2
+        // rounds).  Half that area took twice the rounds, each an LDS write
+        // and read in sequence: 2-3% of C2.  (LDS operations of a wave
+        // complete in order, so a round's reads see its writes and precede
+        // the next round's writes.)
         {
             const float l_run = pair_sum(l_half);
             const float inv = l_run == 0.0f ? 0.0f : 1.0f / l_run;
             const int rr = lane >> 3;
             const int rc = lane & 7;
-            const int r16 = l32 & 15;
-            auto flush = [&](int half, int col_byte) __attribute__((always_inline)) {
+            auto flush = [&](int col_byte) __attribute__((always_inline)) {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                for (int j = 0; j < 4; ++j) {
                     const int r = 8 * j + rr;
                     const u32x4 w = *reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(
                         sO + r * 128 + ((rc ^ (r & 7)) << 4));
-                    const int row = qb * 32 + 16 * half + r;
+                    const int row = qb * 32 + r;
                     // streaming store: O is not read again here (2-3%)
                     if (row < Lq) __builtin_nontemporal_store(w, reinterpret_cast<u32x4 *>(obase + (int64_t)row * o_nb2 + col_byte + rc * 16));
                 }
             };
+            if (o_type == KD_FA_TYPE_F32) {
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                const bool mine = (l32 >> 4) == half;
-                if (o_type == KD_FA_TYPE_F32) {
+                for (int dblk = 0; dblk < 4; ++dblk) {
 #pragma unroll
-                    for (int dblk = 0; dblk < 4; ++dblk) {
-                        if (mine) {
-#pragma unroll
-                            for (int g = 0; g < 4; ++g) {
-                                const f32x4 v = {o[dblk][4 * g] * inv, o[dblk][4 * g + 1] * inv,
-                                                 o[dblk][4 * g + 2] * inv, o[dblk][4 * g + 3] * inv};
-                                *reinterpret_cast<__attribute__((address_space(3))) f32x4 *>(
-                                    sO + r16 * 128 + (((2 * g + hi_b) ^ (r16 & 7)) << 4)) = v;
-                            }
-                        }
-                        flush(half, dblk * 128);
+                    for (int g = 0; g < 4; ++g) {
+                        const f32x4 v = {o[dblk][4 * g] * inv, o[dblk][4 * g + 1] * inv,
+                                         o[dblk][4 * g + 2] * inv, o[dblk][4 * g + 3] * inv};
+                        *reinterpret_cast<__attribute__((address_space(3))) f32x4 *>(
+                            sO + l32 * 128 + (((2 * g + hi_b) ^ (l32 & 7)) << 4)) = v;
                     }
-                } else {
-                    const bool bf = o_type == KD_FA_TYPE_BF16;
+                    flush(dblk * 128);
+                }
+            } else {
+                const bool bf = o_type == KD_FA_TYPE_BF16;
 #pragma unroll
-                    for (int rnd = 0; rnd < 2; ++rnd) {
-                        if (mine) {
+                for (int rnd = 0; rnd < 2; ++rnd) {
 #pragma unroll
-                            for (int dd = 0; dd < 2; ++dd)
+                    for (int dd = 0; dd < 2; ++dd)
 #pragma unroll
-                                for (int g = 0; g < 4; ++g) {
-                                    const int dblk = 2 * rnd + dd;
-                                    const float v0 = o[dblk][4 * g] * inv, v1 = o[dblk][4 * g + 1] * inv;
-                                    const float v2 = o[dblk][4 * g + 2] * inv, v3 = o[dblk][4 * g + 3] * inv;
-                                    const u32x2 w = bf ? (u32x2){Elem<__bf16>::pack2(v0, v1), Elem<__bf16>::pack2(v2, v3)}
-                                                       : (u32x2){Elem<_Float16>::pack2(v0, v1), Elem<_Float16>::pack2(v2, v3)};
-                                    *reinterpret_cast<__attribute__((address_space(3))) u32x2 *>(
-                                        sO + r16 * 128 + (((dd * 4 + g) ^ (r16 & 7)) << 4) + 8 * hi_b) = w;
-                                }
+                        for (int g = 0; g < 4; ++g) {
+                            const int dblk = 2 * rnd + dd;
+                            const float v0 = o[dblk][4 * g] * inv, v1 = o[dblk][4 * g + 1] * inv;
+                            const float v2 = o[dblk][4 * g + 2] * inv, v3 = o[dblk][4 * g + 3] * inv;
+                            const u32x2 w = bf ? (u32x2){Elem<__bf16>::pack2(v0, v1), Elem<__bf16>::pack2(v2, v3)}
+                                               : (u32x2){Elem<_Float16>::pack2(v0, v1), Elem<_Float16>::pack2(v2, v3)};
+                            *reinterpret_cast<__attribute__((address_space(3))) u32x2 *>(
+                                sO + l32 * 128 + (((dd * 4 + g) ^ (l32 & 7)) << 4) + 8 * hi_b) = w;
                         }
-                        flush(half, rnd * 128);
-                    }
+                    flush(rnd * 128);
                 }
             }
         }
