@@ -166,6 +166,35 @@ def test_cross_attention_norm_mask(use_ws):
     assert_parity(gather_rows(out, np.arange(B * H * Lq), H, Lq), orc.fa_f64(q2, k2, v, mask=m), "dit cross")
 
 
+@pytest.mark.parametrize("q_dtype,masked", [(torch.bfloat16, True), (torch.bfloat16, False),
+                                             (torch.float32, True), (torch.float32, False)])
+def test_cross_attention_norm_several_blocks_per_wave(q_dtype, masked):
+    """Short key set with the query norm, 256 (b, h) pairs and 10 query
+    blocks of 32 rows each: one range per pair, so waves 0 and 1 of every
+    workgroup run a second block after storing their first one's O (the
+    query-norm weights are reloaded between the two).  Bitwise equal to the
+    node on the pre-normalised operands, and the oracle on sampled rows."""
+    _need_gpu()
+    _announce(f"dit cross-attention norm, 2 blocks per wave, q {q_dtype}, mask {masked}")
+    B, H, Lq, Lk = 1, 256, 300, 77
+    q, k, v = qkv(B, H, Lq, Lk, torch.bfloat16, seed=93, q_dtype=q_dtype)
+    m = padding_mask(B, Lq, Lk, (61,)) if masked else None
+    wq, wk = _weights(94)
+    norm = kd_fa.qk_norm(wq.to(DEV), wk.to(DEV), EPS)
+    qg, kg, vg = q.to(DEV), k.to(DEV), v.to(DEV)
+    mg = None if m is None else m.to(DEV)
+    ws = torch.empty(k.numel(), dtype=torch.bfloat16, device=DEV)
+    out = kd_fa.flash_attn_ext(qg, kg, vg, mask=mg, norm=norm, workspace=ws)
+    o16 = kd_fa.flash_attn_ext(qg, kg, vg, mask=mg, norm=norm, workspace=ws, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    q2 = _norm(q, wq).to(torch.bfloat16)
+    k2 = _norm(k, wk).to(torch.bfloat16)
+    assert torch.equal(out, _plain(q2, k2, v, m))
+    assert torch.equal(o16, out.to(torch.bfloat16))
+    rows = sample_rows(B, H, Lq, 2, 95)   # row 299 of each head: block 9, wave 1's second
+    assert_parity(gather_rows(out, rows, H, Lq), orc.fa_f64(q2, k2, v, mask=m, rows=rows), "dit cross, 2 blocks per wave")
+
+
 def test_norm_of_one_side_only():
     """A NULL weight leaves that side as it is."""
     _need_gpu()
