@@ -295,7 +295,9 @@ enum {
     KD_FA_ROUTE_NO_XRES = 2,   /* short key sets: the 32-row kernel, not the LDS-resident */
     KD_FA_ROUTE_D512_R1 = 4,   /* D = 512: one 32-row block per workgroup                 */
     KD_FA_ROUTE_NO_SPLIT = 8,  /* short query sets: no key split (one pass per row)      */
-    KD_FA_ROUTE_W64_SHORT = 16 /* unmasked key sets <= 896 too: the 64-row kernel        */
+    KD_FA_ROUTE_W64_SHORT = 16, /* unmasked key sets <= 896 too: the 64-row kernel       */
+    KD_FA_ROUTE_STAGED = 32     /* K transformed without a workspace: staged whenever the
+                                   shape allows, also where one on-load launch is cheaper */
 };
 int kd_fa_set_routing(int flags);
 

@@ -253,24 +253,33 @@ kdfa::Args head_range(const kdfa::Args &a, int b, int h0, int n) {
 }
 
 // Group sizes for run_staged, first to last (the last one rotates K on
-// load).  A launch fills the GPU in rounds of one workgroup per CU (256 on
-// MI355X), one workgroup per 256 query rows and head, and its last round may
-// be partial; the sizes minimise the rounds of all launches (plus a small
-// cost per launch pair; the on-load kernel's rounds count 1.4 times) under
-// the constraints: each group at most `ratio` times the heads of the next
-// (whose output rows hold its transformed K) and within one batch; the last
-// group has 1 to 8 heads.  A dynamic program over (pairs left, size of the
-// next group), O(P^3) per last-group size for P (b, h) pairs, remembered for
-// the last shape of the calling thread.
-std::vector<int> staged_groups(int P, int H, int wg_head, int ratio) {
+// load), and their cost.  A launch fills the GPU in rounds of one workgroup
+// per CU (256 on MI355X), one workgroup per 256 query rows and head, and its
+// last round may be partial; the sizes minimise the rounds of all launches
+// (plus a small cost per launch pair; the on-load kernel's rounds count 1.4
+// times) under the constraints: each group at most `ratio` times the heads
+// of the next (whose output rows hold its transformed K) and within one
+// batch; the last group has 1 to 8 heads.  A dynamic program over (pairs
+// left, size of the next group), O(P^3) per last-group size for P (b, h)
+// pairs, remembered for the last shape of the calling thread.  The cost is
+// in the same units as onload_cost's, the one launch that rotates K on load
+// for every pair.
+constexpr double kStagedLaunch = 0.05, kStagedOnLoad = 1.4;
+double launch_rounds(int heads, int wg_head) { return (double)(((int64_t)heads * wg_head + 255) / 256); }
+double onload_cost(int P, int wg_head) { return kStagedOnLoad * launch_rounds(P, wg_head); }
+struct StagedPlan {
+    std::vector<int> sizes;
+    double cost = 1e300;
+};
+StagedPlan staged_groups(int P, int H, int wg_head, int ratio) {
     struct Memo {
         int P = -1, H = -1, wg = -1, ratio = -1;
-        std::vector<int> sizes;
+        StagedPlan plan;
     };
     thread_local Memo memo;
-    if (memo.P == P && memo.H == H && memo.wg == wg_head && memo.ratio == ratio) return memo.sizes;
-    auto rounds = [wg_head](int h) { return (double)(((int64_t)h * wg_head + 255) / 256); };
-    constexpr double kLaunch = 0.05, kOnLoad = 1.4;
+    if (memo.P == P && memo.H == H && memo.wg == wg_head && memo.ratio == ratio) return memo.plan;
+    auto rounds = [wg_head](int h) { return launch_rounds(h, wg_head); };
+    constexpr double kLaunch = kStagedLaunch, kOnLoad = kStagedOnLoad;
     double best_cost = 1e300;
     std::vector<int> best;
     std::vector<double> dp((size_t)(P + 1) * (P + 1));
@@ -307,14 +316,29 @@ std::vector<int> staged_groups(int P, int H, int wg_head, int ratio) {
             best.push_back(n_last);
         }
     }
-    memo = {P, H, wg_head, ratio, best};
-    return best;
+    memo = {P, H, wg_head, ratio, {best, best_cost}};
+    return memo.plan;
 }
 
-int run_staged(const kdfa::Args &a, int kv_type, hipStream_t hs) {
-    const int H = a.H, P = a.H * a.B;
+// The staged plan of a call that staged_ok allows.
+StagedPlan staged_plan(const kdfa::Args &a) {
     const int ratio = a.o_type == KD_FA_TYPE_F32 ? 2 : 1;   // transformed K rows per output row
-    const std::vector<int> sizes = staged_groups(P, H, (a.Lq + 255) / 256, ratio);
+    return staged_groups(a.H * a.B, a.H, (a.Lq + 255) / 256, ratio);
+}
+
+// Staging pays when its launches take fewer rounds than one launch that
+// rotates K on load for every pair.  When the whole call fits one round
+// (the 1,280-token self-attention: 160 workgroups), each staged launch still
+// takes a whole workgroup lifetime: five launches took 144 us against one
+// on-load launch's 51 us there.  KD_FA_ROUTE_STAGED stages whenever the shape
+// allows (for comparisons).
+bool staged_pays(const kdfa::Args &a, const StagedPlan &plan, int route) {
+    if (plan.sizes.empty()) return false;
+    return (route & KD_FA_ROUTE_STAGED) || plan.cost < onload_cost(a.H * a.B, (a.Lq + 255) / 256);
+}
+
+int run_staged(const kdfa::Args &a, const std::vector<int> &sizes, int kv_type, hipStream_t hs) {
+    const int H = a.H;
     std::vector<int> start(1, 0);
     for (int n : sizes) start.push_back(start.back() + n);
     const int n_last = sizes.back();
@@ -414,7 +438,10 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
         return kdfa::launch_d512(a, d->v.type, rows, hs) == hipSuccess ? KD_FA_OK : KD_FA_ERR_LAUNCH;
     }
     bool k_rope = k_xform && !ws;
-    if (k_rope && staged_ok(a, d, route)) return run_staged(a, d->v.type, hs);
+    if (k_rope && staged_ok(a, d, route)) {
+        const StagedPlan plan = staged_plan(a);
+        if (staged_pays(a, plan, route)) return run_staged(a, plan.sizes, d->v.type, hs);
+    }
     // a mask row block shared by every head is read once per q-tile when the
     // heads of a q-tile run back to back (K and V of all heads then share the
     // L2 instead, which the short text keys of the cross-attention allow)

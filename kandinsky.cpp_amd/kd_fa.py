@@ -59,6 +59,7 @@ ROUTE_NO_XRES = 2
 ROUTE_D512_R1 = 4
 ROUTE_NO_SPLIT = 8
 ROUTE_W64_SHORT = 16
+ROUTE_STAGED = 32
 
 
 class KdFaTensor(ctypes.Structure):

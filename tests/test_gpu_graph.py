@@ -97,6 +97,13 @@ class Layer:
 def test_layer_calls_replay_bitwise():
     _need_gpu()
     _announce("graph capture: staged rope_run, dit_run_static, masked cross-attn, q8_0 linear")
+    # this shape fits one round of workgroups, where kd_fa_rope_run would be
+    # one on-load launch: ROUTE_STAGED keeps its staged launch sequence
+    with kd_fa.routing(kd_fa.ROUTE_STAGED):
+        _replay_layer()
+
+
+def _replay_layer():
     layer = Layer()
     eager_out, graph_out = layer.outputs(), layer.outputs()
     run_eager, keep_e = layer.calls(eager_out)

@@ -66,13 +66,18 @@ def test_staged_equals_workspace(case):
     q, k, v = (t.to(DEV) for t in qkv(B, H, L, L, kt, seed=B * 100 + H, q_dtype=qt))
     rope = _rope(mode, T, Hp, Wp)
     ws = torch.empty(k.numel(), dtype=kt, device=DEV)
-    staged = kd_fa.flash_attn_ext(q, k, v, rope=rope, out_dtype=ot)
+    # these shapes fit one round of workgroups, where the default choice is
+    # one launch rotating K on load; ROUTE_STAGED stages them anyway
+    with kd_fa.routing(kd_fa.ROUTE_STAGED):
+        staged = kd_fa.flash_attn_ext(q, k, v, rope=rope, out_dtype=ot)
+    default = kd_fa.flash_attn_ext(q, k, v, rope=rope, out_dtype=ot)
     viaws = kd_fa.flash_attn_ext(q, k, v, rope=rope, workspace=ws, out_dtype=ot)
     with kd_fa.routing(kd_fa.ROUTE_NO_W64):
         onload = kd_fa.flash_attn_ext(q, k, v, rope=rope, out_dtype=ot)
     torch.cuda.synchronize()
     assert torch.equal(staged, viaws)
     assert torch.equal(staged, onload)
+    assert torch.equal(default, viaws)
     if mode == "table":
         tab = torch.from_numpy(kd_fa.visual_rope_table(T, Hp, Wp, AXES, SCALE_FACTOR, THETA))
         rows = sample_rows(B, H, L, 40, seed=H)
@@ -93,10 +98,13 @@ def test_staged_norm_and_rope_equals_workspace():
     norm = kd_fa.qk_norm(wq, wk, 1e-6)
     rope = _rope("table", T, Hp, Wp)
     ws = torch.empty(k.numel(), dtype=k.dtype, device=DEV)
-    a = kd_fa.flash_attn_ext(q, k, v, rope=rope, norm=norm)
+    with kd_fa.routing(kd_fa.ROUTE_STAGED):
+        a = kd_fa.flash_attn_ext(q, k, v, rope=rope, norm=norm)
+    a1 = kd_fa.flash_attn_ext(q, k, v, rope=rope, norm=norm)   # one launch, K on load
     b = kd_fa.flash_attn_ext(q, k, v, rope=rope, norm=norm, workspace=ws)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+    assert torch.equal(a1, b)
 
 
 def test_staged_production_shape():
