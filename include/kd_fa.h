@@ -152,6 +152,23 @@ int kd_fa_supports(const kd_fa_desc *desc, int *reason);
 int kd_fa_run(const kd_fa_desc *desc, void *stream);
 
 /*
+ * kd_fa_run_ws - kd_fa_run with a caller workspace, as ggml's backend
+ * kernels take scratch from the backend's buffer pool while the node runs
+ * (ggml_backend_graph_compute, src/core/executor.hpp:241): a masked node
+ * whose key set is short (Lk <= 256: the text cross-attention,
+ * src/models/crossdit.hpp:174-200) keeps in it a summary of which 64-key
+ * tiles of its mask hold finite values for each 32-row block of queries,
+ * written by a pass over the mask on `stream`, so that the attention skips
+ * the fully masked tiles of a block without loading their mask rows.  The
+ * result is bitwise kd_fa_run's.  With workspace_bytes below
+ * kd_fa_workspace_size(desc, NULL, NULL), or for other nodes, the call is
+ * kd_fa_run.  workspace must be 16-byte aligned (KD_FA_ERR_LAYOUT); its
+ * contents need not be initialised, and calls that overlap on one buffer
+ * race.  The library still allocates nothing.
+ */
+int kd_fa_run_ws(const kd_fa_desc *desc, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * kd_fa_rope_run - rope::apply(q), rope::apply(k) (src/rope.hpp:109-155,
  * as DiTSelfAttention::forward calls it, src/models/crossdit.hpp:139-142)
  * fused into kd_fa_run.  The result is defined as kd_fa_run on
@@ -213,11 +230,23 @@ typedef struct kd_fa_qk_norm {
  * type, the reference's order (ops.hpp:167 casts after RoPE) -- when K is
  * transformed (a K norm weight or a RoPE mode); the workspace is then
  * mandatory (KD_FA_ERR_NULL without one).  kd_fa_dit_supports accepts an
- * F32 K on exactly that condition.
- * norm == NULL and rope == NULL is kd_fa_run.
+ * F32 K on exactly that condition.  With kd_fa_workspace_size(desc, rope,
+ * norm) bytes, a masked short-key node (the cross-attention) also keeps its
+ * mask summary there, after K (as kd_fa_run_ws).
+ * norm == NULL and rope == NULL is kd_fa_run (kd_fa_run_ws with a
+ * workspace).
  */
 int kd_fa_dit_run(const kd_fa_desc *desc, const kd_fa_rope *rope, const kd_fa_qk_norm *norm,
                   void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Bytes of workspace kd_fa_run_ws, kd_fa_rope_run_ws and kd_fa_dit_run can
+ * use for the node (0 for an invalid node or one that uses none): the
+ * transformed K (kd_fa_rope_workspace_size bytes) when rope or a key norm
+ * transforms K, then, 256-byte aligned, the mask summary of a masked
+ * short-key node (4 bytes per mask batch, mask head and 32 query rows).
+ */
+size_t kd_fa_workspace_size(const kd_fa_desc *desc, const kd_fa_rope *rope, const kd_fa_qk_norm *norm);
 
 /* kd_fa_rope_supports plus the checks of the norm descriptor.  Host-only. */
 int kd_fa_dit_supports(const kd_fa_desc *desc, const kd_fa_rope *rope,

@@ -157,6 +157,18 @@ size_t rope_ws_bytes(const kd_fa_desc *d) {
            elem_size(d->v.type);
 }
 
+// The workspace holds the transformed K (when K is transformed) and, after
+// it at a 256-byte boundary, the mask summary of a masked call whose key set
+// the short-key kernel can hold (one 32-bit word per mask batch, mask head
+// and 32-row query block).
+size_t summary_offset(const kd_fa_desc *d, bool k_xform) {
+    return k_xform ? (rope_ws_bytes(d) + 255) / 256 * 256 : 0;
+}
+size_t summary_bytes(const kd_fa_desc *d, bool rope_on) {
+    if (!d->mask.data || rope_on || d->q.ne[0] != kHeadDim || d->k.ne[1] > kdfa::kXresMaxKeys) return 0;
+    return 4 * (size_t)d->mask.ne[3] * (size_t)d->mask.ne[2] * (size_t)((d->q.ne[1] + 31) / 32);
+}
+
 // K is transformed (normalised and / or rotated) when a norm weight or a
 // RoPE mode asks for it: with ws != nullptr once into ws (contiguous, K's
 // type), after which the attention transforms only Q on load; without, group
@@ -329,8 +341,8 @@ StagedPlan staged_plan(const kdfa::Args &a) {
 // Staging pays when its launches take fewer rounds than one launch that
 // rotates K on load for every pair.  When the whole call fits one round
 // (the 1,280-token self-attention: 160 workgroups), each staged launch still
-// takes a whole workgroup lifetime: five launches took 144 us against one
-// on-load launch's 51 us there.  KD_FA_ROUTE_STAGED stages whenever the shape
+// takes a whole workgroup lifetime: its five launches took 144 us there, one
+// on-load launch for all 32 heads 55 us.  KD_FA_ROUTE_STAGED stages whenever the shape
 // allows (for comparisons).
 bool staged_pays(const kdfa::Args &a, const StagedPlan &plan, int route) {
     if (plan.sizes.empty()) return false;
@@ -376,9 +388,8 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
     if (st != KD_FA_OK) return st;
     // an F32 K is rounded to V's type by the workspace pre-pass only
     if (!ws && k_xform && d->k.type == KD_FA_TYPE_F32) return KD_FA_ERR_NULL;
-    if (ws && k_xform) {
-        if (!is_16b(ws) || ws_bytes < rope_ws_bytes(d)) return KD_FA_ERR_LAYOUT;
-    }
+    if (ws && !is_16b(ws)) return KD_FA_ERR_LAYOUT;
+    if (ws && k_xform && ws_bytes < rope_ws_bytes(d)) return KD_FA_ERR_LAYOUT;
     const int route = g_route.load(std::memory_order_relaxed);
     const int64_t Lq = d->q.ne[1], H = d->q.ne[2], B = d->q.ne[3];
     if (Lq == 0 || H == 0 || B == 0) return KD_FA_OK;
@@ -460,6 +471,16 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
     hipError_t e;
     if (use_xres(a, d, k_rope, route)) {
         xres_split(a);
+        // with room in the workspace, the mask summary: tiles that are -inf
+        // for all rows of a block are then skipped without loading their
+        // mask chunks (one L2 round trip per dead tile and block)
+        const size_t s_off = summary_offset(d, k_xform), s_bytes = summary_bytes(d, rope_on);
+        if (a.m && ws && s_bytes && ws_bytes >= s_off + s_bytes) {
+            uint32_t *sum = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + s_off);
+            if (kdfa::launch_mask_live(a, sum, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
+            a.m_live = sum;
+            a.m_live_nqb = (int32_t)((Lq + 31) / 32);
+        }
         e = kdfa::launch_xres(a, d->v.type, hs);
     } else if (use_w64(a, k_rope, route)) {
         a.n_qt = (int32_t)((Lq + kdfa::kW64Rows - 1) / kdfa::kW64Rows);
@@ -503,6 +524,16 @@ size_t k_workspace_need(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk
     if (*status != KD_FA_OK || !k_xform || d->q.ne[0] != kHeadDim) return 0;
     return rope_ws_bytes(d);
 }
+
+size_t workspace_need(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, int *status) {
+    const bool rope_on = r && r->mode != KD_FA_ROPE_NONE;
+    const bool k_xform = rope_on || (n && n->k_weight);
+    *status = validate(d, r, n, nullptr, k_xform);
+    if (*status != KD_FA_OK) return 0;
+    const size_t k_need = k_xform && d->q.ne[0] == kHeadDim ? rope_ws_bytes(d) : 0;
+    const size_t s_need = summary_bytes(d, rope_on);
+    return s_need ? summary_offset(d, k_need != 0) + s_need : k_need;
+}
 }  // namespace kdfa
 
 extern "C" {
@@ -520,6 +551,17 @@ int kd_fa_rope_supports(const kd_fa_desc *desc, const kd_fa_rope *rope, int *rea
 }
 
 int kd_fa_run(const kd_fa_desc *desc, void *stream) { return run(desc, nullptr, nullptr, nullptr, 0, stream); }
+
+int kd_fa_run_ws(const kd_fa_desc *desc, void *workspace, size_t workspace_bytes, void *stream) {
+    return run(desc, nullptr, nullptr, workspace, workspace_bytes, stream);
+}
+
+size_t kd_fa_workspace_size(const kd_fa_desc *desc, const kd_fa_rope *rope, const kd_fa_qk_norm *norm) {
+    if (!desc) return 0;
+    int st = KD_FA_OK;
+    const size_t need = kdfa::workspace_need(desc, rope, norm, &st);
+    return st == KD_FA_OK ? need : 0;
+}
 
 int kd_fa_rope_run(const kd_fa_desc *desc, const kd_fa_rope *rope, void *stream) {
     return run(desc, rope, nullptr, nullptr, 0, stream);

@@ -45,6 +45,12 @@ struct Args {
     const float *qn_w;    // RMSNorm weight of Q (F32 [128]) or nullptr
     const float *kn_w;    // RMSNorm weight of K (F32 [128]) or nullptr
     float norm_eps;
+    // fa_fwd_xres with a mask: per (mask batch, mask head, 32-row query
+    // block), bit t set when key tile t holds a finite mask value for a row
+    // of the block (launch_mask_live), or nullptr (every tile checked by
+    // loading its mask chunks)
+    const uint32_t *m_live;
+    int32_t m_live_nqb;   // 32-row query blocks per (mask batch, mask head)
 };
 
 // KD_FA_OK when the current device is a gfx950 (checked once per device),
@@ -58,6 +64,10 @@ int run_node(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, v
 // Bytes of K-sized workspace the node needs (0 when K is not transformed);
 // *status gets the node's validation status (host-only).
 size_t k_workspace_need(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, int *status);
+
+// Bytes of workspace the node can use (kd_fa_workspace_size): the
+// transformed K, then the mask summary of a masked short-key call.
+size_t workspace_need(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, int *status);
 
 // Enqueue the 32-row kernel for K/V element type kv_type on `stream`, with
 // `waves` waves of 32 query rows per workgroup (d128_waves; a.n_qt and
@@ -75,6 +85,14 @@ hipError_t launch_w64(const Args &a, int kv_type, hipStream_t stream);
 // query blocks per (b, h).
 constexpr int kXresMaxKeys = 256;
 hipError_t launch_xres(const Args &a, int kv_type, hipStream_t stream);
+
+// Enqueue the mask summary fa_fwd_xres reads through a.m_live: one 32-bit
+// word per (mask batch, mask head, 32-row query block) of the call's mask
+// (rows past Lq clamped to Lq - 1, keys below Lk, Lk <= kXresMaxKeys, rows
+// 16-byte aligned), bit t set when 64-key tile t holds a value other than
+// -inf; written to `out` (mask_live_words(a) words).
+int64_t mask_live_words(const Args &a);
+hipError_t launch_mask_live(const Args &a, uint32_t *out, hipStream_t stream);
 
 // Enqueue the D = 512 kernel (no mask, no RoPE; 32-row query tiles).
 // rows: query rows per workgroup, 32 or 64 (a.n_qt and a.n_blocks counted in

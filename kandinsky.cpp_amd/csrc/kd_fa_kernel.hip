@@ -1026,6 +1026,15 @@ void fa_fwd_xres(Args a) {
 
     f32x16 o[4];
     float m_run, l_half;
+    // the block's live key tiles (bit t: tile t holds a finite mask value
+    // for one of its rows), from the mask summary when the call has one,
+    // else every tile (each is then checked on its mask chunks); the mask
+    // chunks of the next live tile are loaded while a tile is computed
+    uint32_t live = 0xfu;
+    auto next_live = [&](int t) __attribute__((always_inline)) -> int {
+        const uint32_t rest = live >> (t + 1);
+        return rest ? t + 1 + (int)__builtin_ctz(rest) : kXNT;
+    };
 
     auto qk = [&](const lds_t *ks_, f32x16 &s0, f32x16 &s1) __attribute__((always_inline)) {
         constexpr int kKPre = HAS_MASK ? 1 : KD_FA_KPRE;
@@ -1117,8 +1126,9 @@ void fa_fwd_xres(Args a) {
                 for (int e = 0; e < 4; ++e)
                     any |= (mr[c][e] & 0xffffu) != 0xfc00u || (mr[c][e] >> 16) != 0xfc00u;
         }
+        const int tn = next_live(t);
         if (__builtin_amdgcn_ballot_w64(any) == 0) {
-            if (t + 1 < n_tiles) issue_m(mrow, t + 1, mr);
+            if (tn < n_tiles) issue_m(mrow, tn, mr);
             return;
         }
         f32x16 s0, s1;
@@ -1134,8 +1144,8 @@ void fa_fwd_xres(Args a) {
             const float mv = mval(i);
             p[i] = mv == -INFINITY ? -INFINITY : __builtin_fmaf(mv, kLog2e, p[i] * c2);
         }
-        // the mask chunks are consumed: the registers take the next tile's
-        if (t + 1 < n_tiles) issue_m(mrow, t + 1, mr);
+        // the mask chunks are consumed: the registers take the next live tile's
+        if (tn < n_tiles) issue_m(mrow, tn, mr);
         update_max(pair_max(max32(p)));
         const float mu = m_run == -INFINITY ? 0.0f : m_run;
 #pragma unroll
@@ -1197,6 +1207,10 @@ void fa_fwd_xres(Args a) {
             args_ptr ap = (args_ptr)__builtin_amdgcn_kernarg_segment_ptr();
             asm volatile("" : "+s"(ap));
             load_uniforms(ap);
+            // the block's word of the mask summary (read here, from the
+            // argument segment, like the other uniforms of the block)
+            const uint32_t *ml = ap->m_live;
+            live = ml ? ml[((int64_t)(b % ap->m_ne3) * ap->m_ne2 + h % ap->m_ne2) * ap->m_live_nqb + qb] : 0xfu;
         }
         lk_b = Lk;
         hi_b = hi;
@@ -1213,7 +1227,8 @@ void fa_fwd_xres(Args a) {
         const uint16_t *mrow = nullptr;
         if (HAS_MASK) {
             mrow = reinterpret_cast<const uint16_t *>(mbase + (int64_t)q_ld * m_nb1);
-            issue_m(mrow, 0, mraw);
+            const int t0 = live ? (int)__builtin_ctz(live) : kXNT;
+            if (t0 < n_tiles) issue_m(mrow, t0, mraw);
         }
         q_frags(qw);
 #pragma unroll
@@ -1222,7 +1237,7 @@ void fa_fwd_xres(Args a) {
         l_half = 0.0f;
 #pragma unroll
         for (int t = 0; t < kXNT; ++t) {
-            if (t < n_tiles) {
+            if (t < n_tiles && ((live >> t) & 1u)) {
                 const bool part = (t + 1) * kBN > lk_b;   // the last tile, keys past Lk
                 if (HAS_MASK) {
                     if (part)
@@ -1253,12 +1268,17 @@ void fa_fwd_xres(Args a) {
             const float inv = l_run == 0.0f ? 0.0f : 1.0f / l_run;
             const int rr = lane >> 3;
             const int rc = lane & 7;
+            // row 8j + rr, chunk rc ^ rr: one base per lane, computed here
+            // from an opaque copy of the lane index (hoisted out of the
+            // block loop, the per-row addresses went to scratch)
+            int ln_f = lane;
+            asm volatile("" : "+v"(ln_f));
+            const lds_t *const fbase = sO + (ln_f >> 3) * 128 + (((ln_f & 7) ^ (ln_f >> 3 & 7)) << 4);
             auto flush = [&](int col_byte) __attribute__((always_inline)) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int r = 8 * j + rr;
-                    const u32x4 w = *reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(
-                        sO + r * 128 + ((rc ^ (r & 7)) << 4));
+                    const u32x4 w = *reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(fbase + j * 1024);
                     const int row = qb * 32 + r;
                     // streaming store: O is not read again here (2-3%)
                     if (row < Lq) __builtin_nontemporal_store(w, reinterpret_cast<u32x4 *>(obase + (int64_t)row * o_nb2 + col_byte + rc * 16));
@@ -1297,6 +1317,64 @@ void fa_fwd_xres(Args a) {
             }
         }
     }
+}
+
+// ---------------------------------------------------------------------------
+// mask_live_kernel: the mask summary of fa_fwd_xres.  One wave per (mask
+// batch, mask head, 32-row query block): lane l reads row l % 32 of the
+// block (rows past Lq clamped to Lq - 1, as the attention reads them),
+// keys 128 * (l / 32) .. +127 below Lk in 16-byte chunks (the mask rows hold
+// every chunk that starts below Lk), and the wave's ballot per tile sets
+// bit t of the block's word when one of those F16 values is not -inf
+// (0xfc00) -- the test fa_fwd_xres applies to a tile's chunks, so a tile
+// the summary marks dead is exactly one it would skip after loading them.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void mask_live_kernel(Args a, uint32_t *out, int64_t n_words) {
+    const int lane = threadIdx.x & 63;
+    const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (w >= n_words) return;
+    const int qb = (int)(w % a.m_live_nqb);
+    const int64_t hb = w / a.m_live_nqb;
+    const int mh = (int)(hb % a.m_ne2);
+    const int mb = (int)(hb / a.m_ne2);
+    const int row = min(qb * 32 + (lane & 31), a.Lq - 1);
+    const int half = lane >> 5;
+    const uint16_t *mrow = reinterpret_cast<const uint16_t *>(a.m + (int64_t)mb * a.m_nb3 + (int64_t)mh * a.m_nb2 +
+                                                              (int64_t)row * a.m_nb1);
+    uint32_t bits = 0;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {   // tile 2 * half + j
+        bool any = false;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const int k0 = (2 * half + j) * kBN + 8 * c;
+            if (k0 < a.Lk) {
+                const u32x4 v = ld16(mrow + k0);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t h16 = (v[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+                    any |= k0 + e < a.Lk && h16 != 0xfc00u;
+                }
+            }
+        }
+        const uint64_t bal = __builtin_amdgcn_ballot_w64(any);
+        bits |= ((uint32_t)(bal & 0xffffffffu) != 0 ? 1u : 0u) << j;          // tile j (lanes 0-31)
+        bits |= ((uint32_t)(bal >> 32) != 0 ? 1u : 0u) << (2 + j);           // tile 2 + j (lanes 32-63)
+    }
+    if (lane == 0) out[w] = bits;
+}
+
+int64_t mask_live_words(const Args &a) {
+    return (int64_t)a.m_ne3 * a.m_ne2 * (((int64_t)a.Lq + 31) / 32);
+}
+
+hipError_t launch_mask_live(const Args &a, uint32_t *out, hipStream_t stream) {
+    const int64_t n = mask_live_words(a);
+    if (n == 0) return hipSuccess;
+    Args s = a;
+    s.m_live_nqb = (int32_t)((a.Lq + 31) / 32);
+    hipLaunchKernelGGL(mask_live_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, stream, s, out, n);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------

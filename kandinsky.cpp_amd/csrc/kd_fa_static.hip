@@ -8,8 +8,9 @@
 // taken once per device, with that device current, by hipGetSymbolAddress on
 // the entry point's first call there; host code then uses only that address
 // (the array's name in host code is a host-side stand-in, not device
-// memory).  The K pre-pass overwrites every byte of the workspace it uses
-// before the attention reads it, so nothing has to start at zero; two calls
+// memory).  The K pre-pass and the mask summary pass overwrite every byte
+// of the workspace they use before the attention reads it, so nothing has
+// to start at zero; two calls
 // that overlap on one GPU (e.g. on two streams) share the array and race.
 #include <hip/hip_runtime.h>
 
@@ -51,9 +52,13 @@ int scratch_ptr(void **out) {
 extern "C" int kd_fa_dit_run_static(const kd_fa_desc *desc, const kd_fa_rope *rope, const kd_fa_qk_norm *norm,
                                     void *stream) {
     int st = KD_FA_OK;
-    const size_t need = kdfa::k_workspace_need(desc, rope, norm, &st);
+    const size_t k_need = kdfa::k_workspace_need(desc, rope, norm, &st);
     if (st != KD_FA_OK) return st;
-    if (need > KD_FA_STATIC_SCRATCH_BYTES) return KD_FA_ERR_SCRATCH;
+    if (k_need > KD_FA_STATIC_SCRATCH_BYTES) return KD_FA_ERR_SCRATCH;
+    // the transformed K and the mask summary of a masked short-key node; a
+    // summary that does not fit is left out (the call then loads the mask
+    // chunks of every tile, with the same result)
+    const size_t need = kdfa::workspace_need(desc, rope, norm, &st);
     if (need == 0) return kdfa::run_node(desc, rope, norm, nullptr, 0, stream);
     st = kdfa::device_gfx950();
     if (st != KD_FA_OK) return st;

@@ -137,6 +137,10 @@ def _lib():
         lib.kd_fa_rope_supports.restype = ctypes.c_int
         lib.kd_fa_run.argtypes = [P(KdFaDesc), ctypes.c_void_p]
         lib.kd_fa_run.restype = ctypes.c_int
+        lib.kd_fa_run_ws.argtypes = [P(KdFaDesc), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.kd_fa_run_ws.restype = ctypes.c_int
+        lib.kd_fa_workspace_size.argtypes = [P(KdFaDesc), P(KdFaRope), P(KdFaQkNorm)]
+        lib.kd_fa_workspace_size.restype = ctypes.c_size_t
         lib.kd_fa_rope_run.argtypes = [P(KdFaDesc), P(KdFaRope), ctypes.c_void_p]
         lib.kd_fa_rope_run.restype = ctypes.c_int
         lib.kd_fa_rope_run_ws.argtypes = [P(KdFaDesc), P(KdFaRope), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
@@ -319,8 +323,10 @@ def run_desc(desc: KdFaDesc, rope: KdFaRope | None = None, stream=None, workspac
     """Enqueue on `stream` (a torch.cuda.Stream, a raw handle, or None for
     torch's current stream).  With `workspace` (a tensor of at least
     workspace_size(desc) bytes) the RoPE call pre-rotates K into it
-    (kd_fa_rope_run_ws).  With `norm` the call is kd_fa_dit_run.  Returns
-    the status code."""
+    (kd_fa_rope_run_ws); without RoPE the call is kd_fa_run_ws (a masked
+    short-key node keeps its mask summary there, given
+    workspace_size_full(desc) bytes).  With `norm` the call is
+    kd_fa_dit_run.  Returns the status code."""
     torch = _torch()
     if stream is None:
         handle = torch.cuda.current_stream().cuda_stream
@@ -335,6 +341,10 @@ def run_desc(desc: KdFaDesc, rope: KdFaRope | None = None, stream=None, workspac
         return _lib().kd_fa_dit_run(ctypes.byref(desc), ctypes.byref(rope) if rope is not None else None,
                                     ctypes.byref(norm), ctypes.c_void_p(wp), nbytes, ctypes.c_void_p(handle))
     if rope is None:
+        if workspace is not None:
+            nbytes = workspace.numel() * workspace.element_size()
+            return _lib().kd_fa_run_ws(ctypes.byref(desc), ctypes.c_void_p(workspace.data_ptr()), nbytes,
+                                       ctypes.c_void_p(handle))
         return _lib().kd_fa_run(ctypes.byref(desc), ctypes.c_void_p(handle))
     if workspace is not None:
         nbytes = workspace.numel() * workspace.element_size()
@@ -362,6 +372,13 @@ def run_static(desc: KdFaDesc, rope: KdFaRope | None = None, norm: KdFaQkNorm | 
 def workspace_size(desc: KdFaDesc) -> int:
     """kd_fa_rope_workspace_size: bytes of K-sized buffer for kd_fa_rope_run_ws."""
     return int(_lib().kd_fa_rope_workspace_size(ctypes.byref(desc)))
+
+
+def workspace_size_full(desc: KdFaDesc, rope: KdFaRope | None = None, norm: KdFaQkNorm | None = None) -> int:
+    """kd_fa_workspace_size: bytes of workspace the node can use (the
+    transformed K, then the mask summary of a masked short-key node)."""
+    return int(_lib().kd_fa_workspace_size(ctypes.byref(desc), ctypes.byref(rope) if rope is not None else None,
+                                           ctypes.byref(norm) if norm is not None else None))
 
 
 def flash_attn_ext(q, k, v, mask=None, scale=None, max_bias=0.0, logit_softcap=0.0,

@@ -237,6 +237,46 @@ def test_workspace_size_and_null_workspace():
     assert kd_fa.lib().kd_fa_rope_run_ws(ctypes.byref(d), ctypes.byref(rope), None, 0, None) == kd_fa.ERR_NULL
 
 
+def test_full_workspace_size_holds_k_then_mask_summary():
+    """kd_fa_workspace_size: the transformed K when K is transformed, then
+    (256-byte aligned) 4 bytes per mask batch, mask head and 32 query rows
+    for a masked node with at most 256 keys; nothing else."""
+    q, k, v, m, dst = _node(B=2, H=8, Lq=100, Lk=77, qt=torch.bfloat16, kt=torch.bfloat16, mask=True)
+    m = torch.zeros((2, 1, 100, 80), dtype=torch.float16)       # rows padded to whole 8-key chunks
+    d = kd_fa.make_desc(q, k, v, m, dst, 0.1)
+    words = 2 * 1 * ((100 + 31) // 32)
+    assert kd_fa.workspace_size_full(d) == 4 * words
+    m8 = torch.zeros((1, 8, 100, 80), dtype=torch.float16)      # per-head mask, batch broadcast
+    assert kd_fa.workspace_size_full(kd_fa.make_desc(q, k, v, m8, dst, 0.1)) == 4 * 8 * ((100 + 31) // 32)
+    wk = torch.ones(128)
+    norm = kd_fa.qk_norm(wk, wk)
+    kbytes = 128 * 77 * 8 * 2 * 2
+    assert kd_fa.workspace_size_full(d, norm=norm) == (kbytes + 255) // 256 * 256 + 4 * words
+    # no mask: K only (or nothing); a mask with more than 256 keys: K only
+    nm = kd_fa.make_desc(q, k, v, None, dst, 0.1)
+    assert kd_fa.workspace_size_full(nm) == 0
+    assert kd_fa.workspace_size_full(nm, norm=norm) == kbytes
+    rope = kd_fa.rope_table(torch.zeros((100, 128)))
+    assert kd_fa.workspace_size_full(nm, rope=rope) == kbytes
+    ql, kl, vl, _, dl = _node(B=1, H=2, Lq=64, Lk=300, qt=torch.bfloat16, kt=torch.bfloat16)
+    ml = torch.zeros((1, 1, 64, 304), dtype=torch.float16)
+    assert kd_fa.workspace_size_full(kd_fa.make_desc(ql, kl, vl, ml, dl, 0.1)) == 0
+    # an invalid node uses none
+    bad = kd_fa.make_desc(q[..., :64], k[..., :64], v[..., :64], None, dst[..., :64], 0.1)
+    assert kd_fa.workspace_size_full(bad) == 0
+
+
+def test_run_ws_checks_workspace_alignment_before_device_work():
+    """kd_fa_run_ws refuses a workspace that is not 16-byte aligned
+    (KD_FA_ERR_LAYOUT) before touching the device; an invalid node keeps its
+    own reason."""
+    q, k, v, m, dst = _node(B=1, H=2, Lq=64, Lk=64, qt=torch.bfloat16, kt=torch.bfloat16, mask=True)
+    d = kd_fa.make_desc(q, k, v, m, dst, 0.1)
+    assert kd_fa.lib().kd_fa_run_ws(ctypes.byref(d), ctypes.c_void_p(4104), 4096, None) == kd_fa.ERR_LAYOUT
+    d = kd_fa.make_desc(q, k, v, m, dst, 0.1, max_bias=1.0)
+    assert kd_fa.lib().kd_fa_run_ws(ctypes.byref(d), ctypes.c_void_p(4096), 4096, None) == kd_fa.ERR_PARAM
+
+
 def test_norm_descriptor_checks():
     q, k, v, m, dst = _node(Lq=60, Lk=60, qt=torch.float32, kt=torch.bfloat16)
     w = torch.ones(132)
