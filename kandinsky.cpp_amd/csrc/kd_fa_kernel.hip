@@ -1321,13 +1321,15 @@ void fa_fwd_xres(Args a) {
 
 // ---------------------------------------------------------------------------
 // mask_live_kernel: the mask summary of fa_fwd_xres.  One wave per (mask
-// batch, mask head, 32-row query block): lane l reads row l % 32 of the
-// block (rows past Lq clamped to Lq - 1, as the attention reads them),
-// keys 128 * (l / 32) .. +127 below Lk in 16-byte chunks (the mask rows hold
-// every chunk that starts below Lk), and the wave's ballot per tile sets
-// bit t of the block's word when one of those F16 values is not -inf
-// (0xfc00) -- the test fa_fwd_xres applies to a tile's chunks, so a tile
-// the summary marks dead is exactly one it would skip after loading them.
+// batch, mask head, 32-row query block); each load instruction reads whole
+// rows: lane l takes 16-byte chunk l % 32 (keys 8 (l % 32) .. +7, tile
+// (l % 32) / 8) of rows 2i + l / 32, i = 0..15 (rows past Lq clamped to
+// Lq - 1, as the attention reads them; chunks that start at or past Lk are
+// not read -- the mask rows hold every chunk that starts below Lk -- and
+// keys past Lk in the last chunk do not count).  The wave's ballot sets bit
+// t of the block's word when one of tile t's F16 values is not -inf
+// (0xfc00): the test fa_fwd_xres applies to a tile's chunks, so a tile the
+// summary marks dead is exactly one it would skip after loading them.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void mask_live_kernel(Args a, uint32_t *out, int64_t n_words) {
     const int lane = threadIdx.x & 63;
@@ -1337,30 +1339,31 @@ __global__ __launch_bounds__(256) void mask_live_kernel(Args a, uint32_t *out, i
     const int64_t hb = w / a.m_live_nqb;
     const int mh = (int)(hb % a.m_ne2);
     const int mb = (int)(hb / a.m_ne2);
-    const int row = min(qb * 32 + (lane & 31), a.Lq - 1);
-    const int half = lane >> 5;
-    const uint16_t *mrow = reinterpret_cast<const uint16_t *>(a.m + (int64_t)mb * a.m_nb3 + (int64_t)mh * a.m_nb2 +
-                                                              (int64_t)row * a.m_nb1);
+    const int c = lane & 31;
+    const int k0 = 8 * c;
+    bool any = false;
+    if (k0 < a.Lk) {
+        const char *base = a.m + (int64_t)mb * a.m_nb3 + (int64_t)mh * a.m_nb2 + (int64_t)k0 * 2;
+        u32x4 v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int row = min(qb * 32 + 2 * i + (lane >> 5), a.Lq - 1);
+            v[i] = ld16(base + (int64_t)row * a.m_nb1);
+        }
+        const int n_keys = min(8, a.Lk - k0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t h16 = (v[i][e >> 1] >> (16 * (e & 1))) & 0xffffu;
+                any |= e < n_keys && h16 != 0xfc00u;
+            }
+    }
+    const uint64_t bal = __builtin_amdgcn_ballot_w64(any);
+    const uint32_t per_chunk = (uint32_t)bal | (uint32_t)(bal >> 32);   // bit c: chunk c of some row
     uint32_t bits = 0;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {   // tile 2 * half + j
-        bool any = false;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const int k0 = (2 * half + j) * kBN + 8 * c;
-            if (k0 < a.Lk) {
-                const u32x4 v = ld16(mrow + k0);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const uint32_t h16 = (v[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-                    any |= k0 + e < a.Lk && h16 != 0xfc00u;
-                }
-            }
-        }
-        const uint64_t bal = __builtin_amdgcn_ballot_w64(any);
-        bits |= ((uint32_t)(bal & 0xffffffffu) != 0 ? 1u : 0u) << j;          // tile j (lanes 0-31)
-        bits |= ((uint32_t)(bal >> 32) != 0 ? 1u : 0u) << (2 + j);           // tile 2 + j (lanes 32-63)
-    }
+    for (int t = 0; t < 4; ++t) bits |= ((per_chunk >> (8 * t)) & 0xffu ? 1u : 0u) << t;
     if (lane == 0) out[w] = bits;
 }
 
