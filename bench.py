@@ -280,7 +280,8 @@ def main():
         mx[1, :, :, :40] = 0
         ox = torch.empty((B, L, HEADS, D), device=dev, dtype=torch.float32)
         dx = kd_fa.make_desc(qx, kx, vx, mx, ox, 1.0 / D ** 0.5)
-        msx = time_launches(torch, lambda: kd_fa.run_desc(dx, None, stream), args.steps, args.warmup, stream)
+        wsx = torch.empty(max(kd_fa.workspace_size_full(dx), 16), dtype=torch.uint8, device=dev)
+        msx = time_launches(torch, lambda: kd_fa.run_desc(dx, None, stream, wsx), args.steps, args.warmup, stream)
         print(json.dumps({"cross_attn_ms": round(msx, 4)}))
         return
     if args.linear_only:
@@ -389,12 +390,16 @@ def main():
             ropex = kd_fa.rope_table(torch.from_numpy(tx).to(dev))
             dx = kd_fa.make_desc(qx, kx, vx, None, ox, 1.0 / D ** 0.5)
             wsx = torch.empty(kx.numel(), dtype=kx.dtype, device=dev)
-            n = 20 if tag.startswith("c1") else 3
-            msx = time_launches(torch, lambda: kd_fa.run_desc(dx, ropex, stream, wsx), n, 1, stream)
+            n = 100 if tag.startswith("c1") else 3
+            msx = time_launches(torch, lambda: kd_fa.run_desc(dx, ropex, stream, wsx), n, 3 if n > 3 else 1, stream)
             flx = 4.0 * Bx * HEADS * Lx * Lx * D
             sec[f"self_attn_{tag}_ms"] = round(msx, 4)
             sec[f"self_attn_{tag}_tflops"] = round(flx / (msx * 1e-3) / 1e12, 2)
             sec[f"self_attn_{tag}_pct_bf16_peak"] = round(100.0 * flx / (msx * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2)
+            if tag.startswith("c1"):
+                # kd_fa_rope_run without a workspace: one launch rotating K on load
+                msy = time_launches(torch, lambda: kd_fa.run_desc(dx, ropex, stream), n, 3, stream)
+                sec[f"self_attn_{tag}_no_ws_ms"] = round(msy, 4)
             del qx, kx, vx, ox, wsx
         # a token count that is not a multiple of 64: 768x432, 121 frames ->
         # latent 31 x 54 x 96, patch (1, 2, 2) -> 31 x 27 x 48 = 40,176 tokens,
@@ -420,11 +425,21 @@ def main():
         m2[1, :, :, :40] = 0
         out2 = torch.empty((B, L, HEADS, D), device=dev, dtype=torch.float32)
         d2 = kd_fa.make_desc(q, k2, v2, m2, out2, 1.0 / D ** 0.5)
-        ms2 = time_launches(torch, lambda: kd_fa.run_desc(d2, None, stream), 20, 3, stream)
+        # kd_fa_run_ws: the mask summary pass, then the short-key kernel,
+        # which skips the fully masked key tiles of each 32-row block without
+        # loading their mask rows; kd_fa_run (no workspace) beside it
+        # (10 warmup calls: the first calls after the buffers are allocated
+        # run up to 10% slower)
+        ws2m = torch.empty(max(kd_fa.workspace_size_full(d2), 16), dtype=torch.uint8, device=dev)
+        ms2n = time_launches(torch, lambda: kd_fa.run_desc(d2, None, stream), 50, 10, stream)
+        ms2 = time_launches(torch, lambda: kd_fa.run_desc(d2, None, stream, ws2m), 50, 10, stream)
         bytes2 = (q.numel() + k2.numel() + v2.numel()) * 2 + m2.numel() * 2 + out2.numel() * 4
         sec["cross_attn_ms"] = round(ms2, 4)
         sec["cross_attn_GBps"] = round(bytes2 / (ms2 * 1e-3) / 1e9, 1)
         sec["cross_attn_hbm_frac"] = round(bytes2 / (ms2 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
+        sec["cross_attn_note"] = ("kd_fa_run_ws (mask summary in the workspace); "
+                                  "the measured ceiling for this byte mix is in profiles/hbm_ceiling_probes.txt")
+        sec["cross_attn_no_ws_ms"] = round(ms2n, 4)
         # the reference's own cross-attention operand form (ops.hpp:122-169,
         # crossdit.hpp:198): Q F32, K/V F16, no mask, prompt lengths 77, 300
         # and 512 (the longest after the tokenizer's crop)
@@ -444,8 +459,8 @@ def main():
         del q32, o32
         # the same with query/key RMSNorm and O stored as bf16 for out_layer
         out2b = torch.empty((B, L, HEADS, D), device=dev, dtype=torch.bfloat16)
-        ws2 = torch.empty(k2.numel(), dtype=k2.dtype, device=dev)
         d2b = kd_fa.make_desc(q, k2, v2, m2, out2b, 1.0 / D ** 0.5)
+        ws2 = torch.empty(kd_fa.workspace_size_full(d2b, None, norm), dtype=torch.uint8, device=dev)
         ms2b = time_launches(torch, lambda: kd_fa.run_desc(d2b, None, stream, ws2, norm), 20, 3, stream)
         bytes2b = bytes2 - out2.numel() * 2
         sec["cross_attn_norm_bf16out_ms"] = round(ms2b, 4)
@@ -489,6 +504,19 @@ def main():
             fll = 2.0 * Mx * N_ * K_
             sec[f"linear_{tag}_ms"] = round(msl, 4)
             sec[f"linear_{tag}_tflops"] = round(fll / (msl * 1e-3) / 1e12, 2)
+            if tag == "qkv_bf16w_bf16x":
+                # the library GEMM (hipBLASLt through torch) on the same BF16
+                # operands, with the node's F32 output and with a BF16 one
+                wt = wl.t()
+                for otag, fn in (("f32out", lambda: torch.mm(xl, wt, out_dtype=torch.float32)),
+                                 ("bf16out", lambda: torch.mm(xl, wt))):
+                    try:
+                        msh = time_launches(torch, fn, 10, 2, stream)
+                    except (TypeError, RuntimeError) as exc:
+                        sec[f"linear_{tag}_hipblaslt_{otag}_error"] = str(exc)[:120]
+                        continue
+                    sec[f"linear_{tag}_hipblaslt_{otag}_ms"] = round(msh, 4)
+                    sec[f"linear_{tag}_hipblaslt_{otag}_tflops"] = round(fll / (msh * 1e-3) / 1e12, 2)
             del xl, yl, wl, dl, wsl
         # 60 x (self + cross) with fresh buffers per layer (3 rotating sets)
         sets = [(q, k, v)] + [tuple(rand(torch, (B, HEADS, L, D), 10 * s + j, dev, bf) for j in range(3))
@@ -502,12 +530,12 @@ def main():
             for i in range(60):
                 ds, dc = descs[i % 3]
                 kd_fa.run_desc(ds, rope, stream, ws)
-                kd_fa.run_desc(dc, None, stream)
+                kd_fa.run_desc(dc, None, stream, ws2m)
 
         ms5 = time_launches(torch, layer_stack, 2, 1, stream)
         sec["step_equivalent_ms"] = round(ms5, 2)
-        sec["step_equivalent_note"] = ("60 x (self-attn via kd_fa_rope_run_ws + cross-attn), batch 2 CFG, "
-                                       "3 rotating input sets")
+        sec["step_equivalent_note"] = ("60 x (self-attn via kd_fa_rope_run_ws + cross-attn via kd_fa_run_ws), "
+                                       "batch 2 CFG, 3 rotating input sets")
         res["secondary"] = sec
         del sets, descs
 
