@@ -473,10 +473,16 @@ def main():
             v5 = rand(torch, (1, 1, L5, 512), 43, dev, torch.float16)
             o5 = torch.empty((1, L5, 1, 512), device=dev, dtype=torch.float32)
             d5 = kd_fa.make_desc(q5, k5, v5, None, o5, 512 ** -0.5)
-            ms5v = time_launches(torch, lambda: kd_fa.run_desc(d5, None, stream), 20, 3, stream)
+            # kd_fa_run_ws: with fewer than 256 blocks of 32 query rows the
+            # keys of every row are split into ranges merged through the
+            # workspace (4,096 tokens: two); kd_fa_run beside it
+            ws5 = torch.empty(max(kd_fa.workspace_size_full(d5), 16), dtype=torch.uint8, device=dev)
+            ms5v = time_launches(torch, lambda: kd_fa.run_desc(d5, None, stream, ws5), 20, 10, stream)
+            ms5n = time_launches(torch, lambda: kd_fa.run_desc(d5, None, stream), 20, 10, stream)
             sec[f"vae_attn_{L5}_ms"] = round(ms5v, 4)
             sec[f"vae_attn_{L5}_tflops"] = round(4.0 * L5 * L5 * 512 / (ms5v * 1e-3) / 1e12, 2)
-            del q5, k5, v5, o5
+            sec[f"vae_attn_{L5}_no_ws_ms"] = round(ms5n, 4)
+            del q5, k5, v5, o5, ws5
         # the DiT linear layers (ops::linear) at 63,488 tokens (31,744 x CFG 2):
         # a 4096 x 4096 projection with Q8_0 weights expanded into the
         # workspace on every call, the same with the weights kept as BF16 rows

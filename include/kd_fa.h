@@ -159,10 +159,15 @@ int kd_fa_run(const kd_fa_desc *desc, void *stream);
  * src/models/crossdit.hpp:174-200) keeps in it a summary of which 64-key
  * tiles of its mask hold finite values for each 32-row block of queries,
  * written by a pass over the mask on `stream`, so that the attention skips
- * the fully masked tiles of a block without loading their mask rows.  The
- * result is bitwise kd_fa_run's.  With workspace_bytes below
- * kd_fa_workspace_size(desc, NULL, NULL), or for other nodes, the call is
- * kd_fa_run.  workspace must be 16-byte aligned (KD_FA_ERR_LAYOUT); its
+ * the fully masked tiles of a block without loading their mask rows; the
+ * result is bitwise kd_fa_run's.  The VAE's one-head D = 512 node
+ * (src/models/vae.hpp:60-101) at short token counts (fewer than 256 blocks
+ * of 32 query rows: the 64x64 latent) splits every row's keys into ranges
+ * computed side by side, their partial results kept in the workspace and
+ * merged by a second pass; the result then differs from kd_fa_run's only
+ * by F32 rounding (the ranges' sums are combined in another order).  With
+ * workspace_bytes below kd_fa_workspace_size(desc, NULL, NULL), or for
+ * other nodes, the call is kd_fa_run.  workspace must be 16-byte aligned (KD_FA_ERR_LAYOUT); its
  * contents need not be initialised, and calls that overlap on one buffer
  * race.  The library still allocates nothing.
  */
@@ -244,7 +249,9 @@ int kd_fa_dit_run(const kd_fa_desc *desc, const kd_fa_rope *rope, const kd_fa_qk
  * use for the node (0 for an invalid node or one that uses none): the
  * transformed K (kd_fa_rope_workspace_size bytes) when rope or a key norm
  * transforms K, then, 256-byte aligned, the mask summary of a masked
- * short-key node (4 bytes per mask batch, mask head and 32 query rows).
+ * short-key node (4 bytes per mask batch, mask head and 32 query rows); for
+ * a D = 512 node with a key split, its partial results (2,056 bytes per
+ * query row and key range).
  */
 size_t kd_fa_workspace_size(const kd_fa_desc *desc, const kd_fa_rope *rope, const kd_fa_qk_norm *norm);
 
@@ -323,7 +330,7 @@ enum {
     KD_FA_ROUTE_NO_W64  = 1,   /* unmasked calls: the 32-row kernel, not the 64-row one   */
     KD_FA_ROUTE_NO_XRES = 2,   /* short key sets: the 32-row kernel, not the LDS-resident */
     KD_FA_ROUTE_D512_R1 = 4,   /* D = 512: one 32-row block per workgroup                 */
-    KD_FA_ROUTE_NO_SPLIT = 8,  /* short query sets: no key split (one pass per row)      */
+    KD_FA_ROUTE_NO_SPLIT = 8,  /* D = 512, short query sets: no key split (one pass)     */
     KD_FA_ROUTE_W64_SHORT = 16, /* unmasked key sets <= 896 too: the 64-row kernel       */
     KD_FA_ROUTE_STAGED = 32     /* K transformed without a workspace: staged whenever the
                                    shape allows, also where one on-load launch is cheaper */

@@ -37,6 +37,9 @@ namespace kdfa {
 // re-read by every workgroup) halves.  R = 1 and R = 2 give bitwise equal
 // results: the same products, the same sums of the partial scores, and the
 // row sums combined in the same tree (4 keys per leaf).
+// With a key split (a.n_split > 1, short query sets with a workspace), a
+// workgroup runs only its range of key tiles and leaves the unnormalised O,
+// running max and row sum of its rows for d512_combine.
 constexpr int kD5 = 512;                     // D, four 128-column slices
 constexpr int kD5Keys = 32;                    // keys per tile
 constexpr int kD5SStride = kD5Keys + 4;        // floats per row of a partial-score block (pad)
@@ -63,12 +66,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31;
     const int hi = lane >> 5;
-    const int qt = blockIdx.x % a.n_qt;
-    const int bh = blockIdx.x / a.n_qt;
+    // key split (a.n_split > 1): the grid holds n_split copies of the
+    // unsplit grid, copy s taking keys [s * split_keys, (s + 1) * split_keys)
+    const int split = a.n_split > 1 ? (int)blockIdx.x / a.n_blocks : 0;
+    const int blk = (int)blockIdx.x - split * a.n_blocks;
+    const int qt = blk % a.n_qt;
+    const int bh = blk / a.n_qt;
     const int h = bh % a.H;
     const int b = bh / a.H;
     const int Lk = a.Lk;
-    const int n_tiles = (Lk + kD5Keys - 1) / kD5Keys;
+    const int k_end = a.n_split > 1 ? min((split + 1) * a.split_keys, Lk) : Lk;
+    const int t_begin = a.n_split > 1 ? split * a.split_keys / kD5Keys : 0;
+    const int n_tiles = (k_end + kD5Keys - 1) / kD5Keys;   // one past the range's last tile
     const int col0 = 128 * wave;                  // this wave's columns of D
 
     // Q fragments of the wave's columns (B operands of S_w^T = K_w Q_w^T)
@@ -137,11 +146,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // compiler's own waits for K stay exact (loads complete in order) and
     // V(t) has landed once at most the 16 newer loads are in flight
     vec8 kf[8];
-    if (n_tiles > 0) {
-        issue_v(0, 0);
-        load_k(0, kf);
+    if (n_tiles > t_begin) {
+        issue_v(t_begin, t_begin & 1);
+        load_k(t_begin, kf);
     }
-    for (int t = 0; t < n_tiles; ++t) {
+    for (int t = t_begin; t < n_tiles; ++t) {
         // the Q fragments (read by the matrix unit only) live in AGPRs, so
         // that O, S and the K fragments have the VGPRs to themselves
 #pragma unroll
@@ -181,7 +190,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             }
 #pragma unroll
             for (int e = 0; e < kKeysPerLane; ++e)
-                if (t * kD5Keys + skey + e >= Lk) sc[e] = -INFINITY;
+                if (t * kD5Keys + skey + e >= k_end) sc[e] = -INFINITY;
             float mx = sc[0];
 #pragma unroll
             for (int e = 1; e < kKeysPerLane; ++e) mx = __builtin_fmaxf(mx, sc[e]);
@@ -241,6 +250,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             }
         }
     }
+    if (a.n_split > 1) {
+        // this range's unnormalised O (times exactly 1), running max and row
+        // sum, for launch_d512_combine
+        const int64_t rows = (int64_t)a.B * a.Lq * a.H;
+        Args pa = a;
+        pa.o = reinterpret_cast<char *>(a.part + (int64_t)split * rows * kD5);
+        pa.o_type = KD_FA_TYPE_F32;
+        pa.o_nb1 = kD5 * 4;
+        pa.o_nb2 = (int64_t)a.H * kD5 * 4;
+        pa.o_nb3 = (int64_t)a.Lq * a.H * kD5 * 4;
+#pragma unroll
+        for (int rb = 0; rb < R; ++rb) store_o_row_l(pa, qt * kRows + 32 * rb + l32, h, b, hi, o[rb], 1.0f, col0);
+        const int q_row = qt * kRows + srow;
+        if (lane % kLanesPerRow == 0 && q_row < a.Lq) {   // the softmax lanes of the wave's rows
+            float *ml = a.part + (int64_t)a.n_split * rows * kD5 +
+                        2 * ((int64_t)split * rows + ((int64_t)b * a.Lq + q_row) * a.H + h);
+            ml[0] = m_run;
+            ml[1] = l_run;
+        }
+        return;
+    }
     if (lane % kLanesPerRow == 0) sL[srow] = l_run;
     __syncthreads();
 #pragma unroll
@@ -248,9 +278,54 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         store_o_row_l(a, qt * kRows + 32 * rb + l32, h, b, hi, o[rb], sL[32 * rb + l32], col0);
 }
 
+// d512_combine: dst row r = sum_s w_s O_s / sum_s w_s l_s with
+// w_s = 2^(m_s - max_s m_s) over the key ranges of a split call (running
+// maxima in the exp2 domain, as the kernel keeps them); 128 threads per row,
+// four columns each, F32 arithmetic, then the store_o_row_l rounding.
+__global__ __launch_bounds__(256) void d512_combine(Args a) {
+    const int64_t rows = (int64_t)a.B * a.Lq * a.H;
+    const int64_t r = (int64_t)blockIdx.x * 2 + (threadIdx.x >> 7);
+    if (r >= rows) return;
+    const int c = (int)(threadIdx.x & 127) * 4;
+    const int S = a.n_split;
+    const float *ml = a.part + (int64_t)S * rows * kD5;
+    float M = -INFINITY;
+    for (int s = 0; s < S; ++s) M = __builtin_fmaxf(M, ml[2 * ((int64_t)s * rows + r)]);
+    float L = 0.0f;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s = 0; s < S; ++s) {
+        const float m = ml[2 * ((int64_t)s * rows + r)];
+        const float w = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
+        L += w * ml[2 * ((int64_t)s * rows + r) + 1];
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(a.part + ((int64_t)s * rows + r) * kD5 + c);
+        acc.x += w * v.x; acc.y += w * v.y; acc.z += w * v.z; acc.w += w * v.w;
+    }
+    const float inv = L == 0.0f ? 0.0f : 1.0f / L;
+    const f32x4 v = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
+    const int h = (int)(r % a.H);
+    const int i = (int)((r / a.H) % a.Lq);
+    const int b = (int)(r / ((int64_t)a.H * a.Lq));
+    char *op = a.o + (int64_t)b * a.o_nb3 + (int64_t)i * a.o_nb2 + (int64_t)h * a.o_nb1;
+    if (a.o_type == KD_FA_TYPE_F32) {
+        *reinterpret_cast<f32x4 *>(op + c * 4) = v;
+    } else if (a.o_type == KD_FA_TYPE_BF16) {
+        *reinterpret_cast<u32x2 *>(op + c * 2) = (u32x2){Elem<__bf16>::pack2(v.x, v.y), Elem<__bf16>::pack2(v.z, v.w)};
+    } else {
+        *reinterpret_cast<u32x2 *>(op + c * 2) =
+            (u32x2){Elem<_Float16>::pack2(v.x, v.y), Elem<_Float16>::pack2(v.z, v.w)};
+    }
+}
+
 template <typename T, int R>
 static hipError_t launch_d512_t(const Args &a, hipStream_t s) {
-    hipLaunchKernelGGL((fa_fwd_d512<T, R>), dim3(a.n_blocks), dim3(256), 0, s, a);
+    const int64_t grid = (int64_t)a.n_blocks * (a.n_split > 1 ? a.n_split : 1);
+    hipLaunchKernelGGL((fa_fwd_d512<T, R>), dim3((unsigned)grid), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_d512_combine(const Args &a, hipStream_t s) {
+    const int64_t rows = (int64_t)a.B * a.Lq * a.H;
+    hipLaunchKernelGGL(d512_combine, dim3((unsigned)((rows + 1) / 2)), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

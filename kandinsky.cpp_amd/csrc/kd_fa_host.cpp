@@ -157,6 +157,33 @@ size_t rope_ws_bytes(const kd_fa_desc *d) {
            elem_size(d->v.type);
 }
 
+// Key split of the D = 512 kernel through the workspace (kd_fa_run_ws):
+// when its 32-row workgroups would leave CUs idle (fewer than 256: the VAE's
+// 64x64 latent, 4,096 tokens, gives 128), each row block's keys are cut into
+// S ranges of whole 32-key tiles (S <= 8, one workgroup per range), whose
+// unnormalised partial results a second pass merges.  `bytes`: the partial
+// O (F32, 512 per row) and running max / row sum of every range and row.
+struct D512Split {
+    int S = 1;
+    int keys = 0;
+    size_t bytes = 0;
+};
+D512Split d512_split(int64_t Lq, int64_t Lk, int64_t H, int64_t B, int route) {
+    D512Split r;
+    const int64_t nb32 = (Lq + 31) / 32 * H * B;
+    if ((route & KD_FA_ROUTE_NO_SPLIT) || nb32 >= 256 || nb32 == 0) return r;
+    const int64_t tiles = (Lk + 31) / 32;
+    int64_t S = std::min<int64_t>(std::min<int64_t>(8, 256 / nb32), tiles);
+    if (S < 2) return r;
+    const int64_t per = (tiles + S - 1) / S;   // tiles per range
+    S = (tiles + per - 1) / per;
+    if (S < 2) return r;
+    r.S = (int)S;
+    r.keys = (int)(per * 32);
+    r.bytes = (size_t)S * (size_t)(Lq * H * B) * (size_t)(kHeadDimVae * 4 + 8);
+    return r;
+}
+
 // The workspace holds the transformed K (when K is transformed) and, after
 // it at a 256-byte boundary, the mask summary of a masked call whose key set
 // the short-key kernel can hold (one 32-bit word per mask batch, mask head
@@ -446,6 +473,16 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
         const int rows = ((route & KD_FA_ROUTE_D512_R1) || (Lq + 63) / 64 * H * B < 256) ? 32 : 64;
         a.n_qt = (int32_t)((Lq + rows - 1) / rows);
         a.n_blocks = (int32_t)(a.n_qt * H * B);
+        // with a workspace, the key split of short query sets (the partial
+        // results, then the merge into dst)
+        const D512Split sp = rows == 32 ? d512_split(Lq, a.Lk, H, B, route) : D512Split{};
+        if (sp.S > 1 && ws && ws_bytes >= sp.bytes) {
+            a.part = static_cast<float *>(ws);
+            a.n_split = sp.S;
+            a.split_keys = sp.keys;
+            if (kdfa::launch_d512(a, d->v.type, rows, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
+            return kdfa::launch_d512_combine(a, hs) == hipSuccess ? KD_FA_OK : KD_FA_ERR_LAUNCH;
+        }
         return kdfa::launch_d512(a, d->v.type, rows, hs) == hipSuccess ? KD_FA_OK : KD_FA_ERR_LAUNCH;
     }
     bool k_rope = k_xform && !ws;
@@ -530,6 +567,7 @@ size_t workspace_need(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_n
     const bool k_xform = rope_on || (n && n->k_weight);
     *status = validate(d, r, n, nullptr, k_xform);
     if (*status != KD_FA_OK) return 0;
+    if (d->q.ne[0] == kHeadDimVae) return d512_split(d->q.ne[1], d->k.ne[1], d->q.ne[2], d->q.ne[3], 0).bytes;
     const size_t k_need = k_xform && d->q.ne[0] == kHeadDim ? rope_ws_bytes(d) : 0;
     const size_t s_need = summary_bytes(d, rope_on);
     return s_need ? summary_offset(d, k_need != 0) + s_need : k_need;

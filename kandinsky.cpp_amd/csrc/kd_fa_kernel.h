@@ -51,6 +51,14 @@ struct Args {
     // loading its mask chunks)
     const uint32_t *m_live;
     int32_t m_live_nqb;   // 32-row query blocks per (mask batch, mask head)
+    // fa_fwd_d512 key split (kd_fa_run_ws): with n_split > 1 each row's keys
+    // are cut into ranges of split_keys (a multiple of 32), and range s of
+    // every row leaves its unnormalised O (F32 [n_split][rows][512]), then
+    // its running max and row sum (F32 [n_split][rows][2]) in `part`, which
+    // launch_d512_combine merges into dst; rows = B * Lq * H, row
+    // (b * Lq + i) * H + h
+    float *part;
+    int32_t n_split, split_keys;
 };
 
 // KD_FA_OK when the current device is a gfx950 (checked once per device),
@@ -98,6 +106,8 @@ hipError_t launch_mask_live(const Args &a, uint32_t *out, hipStream_t stream);
 // rows: query rows per workgroup, 32 or 64 (a.n_qt and a.n_blocks counted in
 // those)
 hipError_t launch_d512(const Args &a, int kv_type, int rows, hipStream_t stream);
+// Merge the key ranges of a split D = 512 call (a.part, a.n_split) into dst.
+hipError_t launch_d512_combine(const Args &a, hipStream_t stream);
 
 // Byte strides of the transformed K the pre-pass writes: per key, per K
 // head, per K batch (contiguous [D, Lk, Hk, Bk]: 256, 256 Lk, 256 Lk Hk).

@@ -144,3 +144,66 @@ def test_d512_vae_128x128_sampled():
     assert torch.equal(out, _run_rows32(q, k, v, scale=D ** -0.5))
     rows = sample_rows(1, 1, L, 32, seed=42)
     assert_parity(gather_rows(out, rows, 1, L), orc.fa_f64(q, k, v, scale=D ** -0.5, rows=rows), "d512 16384")
+
+
+def _split_ranges(Lq, Lk, H, B):
+    """(ranges, keys per range) of the key split kd_fa_run_ws takes for a
+    D = 512 node: fewer than 256 blocks of 32 query rows, at most 8 ranges
+    of whole 32-key tiles, at least two."""
+    nb = (Lq + 31) // 32 * H * B
+    tiles = (Lk + 31) // 32
+    if nb >= 256:
+        return 1, 0
+    S = min(8, 256 // nb, tiles)
+    if S < 2:
+        return 1, 0
+    per = (tiles + S - 1) // S
+    S = (tiles + per - 1) // per
+    return (S, per * 32) if S >= 2 else (1, 0)
+
+
+SPLIT_CASES = [
+    # B, H, Hkv, Bk, Lq, Lk, K/V type, dst type
+    (1, 1, 1, 1, 4096, 4096, torch.float16, torch.float32),    # 64x64 latent: two key ranges
+    (1, 1, 1, 1, 1024, 1024, torch.float16, torch.float32),    # 32x32 latent: eight ranges
+    (1, 1, 1, 1, 300, 1000, torch.bfloat16, torch.float32),    # ragged last tile and range
+    (2, 2, 1, 1, 100, 200, torch.float16, torch.bfloat16),     # GQA and batch broadcast, 16-bit dst
+    (1, 1, 1, 1, 64, 40, torch.float16, torch.float32),        # two tiles: two ranges of one tile
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: f"B{c[0]}H{c[1]}q{c[4]}k{c[5]}{str(c[7])[-4:]}")
+def test_d512_key_split(case):
+    """kd_fa_run_ws on a D = 512 node with few query rows: the keys of every
+    row are split into ranges computed side by side and merged through the
+    workspace.  Parity against the oracle, determinism, the workspace size
+    rule, and with the split routed out the call is bitwise kd_fa_run."""
+    _need_gpu()
+    B, H, Hkv, Bk, Lq, Lk, kt, ot = case
+    _announce(f"d512 key split {case}")
+    q, k, v = _qkv(B, H, Lq, Lk, kt, seed=Lq + Lk + 7, Hkv=Hkv, Bk=Bk)
+    q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+    scale = D ** -0.5
+    outs = [torch.empty((B, Lq, H, D), dtype=ot, device=DEV) for _ in range(4)]
+    descs = [kd_fa.make_desc(q, k, v, None, o, scale) for o in outs]
+    S, _ = _split_ranges(Lq, Lk, H, B)
+    need = kd_fa.workspace_size_full(descs[0])
+    assert S >= 2 and need == S * B * H * Lq * (D * 4 + 8)
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV).fill_(0x7F)
+    assert kd_fa.run_desc(descs[0], workspace=ws) == kd_fa.OK
+    assert kd_fa.run_desc(descs[1], workspace=ws) == kd_fa.OK
+    assert kd_fa.run_desc(descs[2]) == kd_fa.OK
+    with kd_fa.routing(kd_fa.ROUTE_NO_SPLIT):
+        assert kd_fa.run_desc(descs[3], workspace=ws) == kd_fa.OK
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    assert torch.equal(outs[2], outs[3])
+    # each range rounds its weights to the operand type against its own
+    # running max (the unsplit call: against the row's), and the ranges'
+    # sums are merged in another order: the difference is that rounding
+    diff = (outs[0].float() - outs[2].float()).abs().max().item()
+    tol = 1e-2 if ot != torch.float32 else (2e-3 if kt == torch.bfloat16 else 2e-4)
+    assert diff <= tol, diff
+    rows = np.arange(B * H * Lq) if Lq <= 1024 else sample_rows(B, H, Lq, 64, seed=5)
+    ref = orc.fa_f64(q.cpu(), k.cpu(), v.cpu(), scale=scale, rows=rows)
+    assert_parity(gather_rows(outs[0].float(), rows, H, Lq), ref, f"d512 key split {case}")
