@@ -129,6 +129,8 @@ inline bool make_node(const Activation &q, const Activation &k, const Activation
 // rope (optional): rotate Q and K on load (rope::apply, src/rope.hpp:109).
 // norm (optional): the query_norm / key_norm RMSNorm of the attention
 // modules before RoPE (crossdit.hpp:135-136, 192-193).
+// k_workspace (optional, kd_fa_workspace_size bytes): the transformed K,
+// and for a masked cross-attention its mask summary (kd_fa_run_ws).
 inline Result attention(const Activation &q, const Activation &k, const Activation &v,
                         int64_t n_head, void *out, const Mask *mask = nullptr,
                         const kd_fa_rope *rope = nullptr, void *stream = nullptr,
@@ -161,6 +163,8 @@ inline Result attention(const Activation &q, const Activation &k, const Activati
         r.status = kd_fa_rope_run_ws(&d, rope, k_workspace, k_workspace_bytes, stream);
     else if (rope)
         r.status = kd_fa_rope_run(&d, rope, stream);
+    else if (k_workspace)
+        r.status = kd_fa_run_ws(&d, k_workspace, k_workspace_bytes, stream);
     else
         r.status = kd_fa_run(&d, stream);
     return r;
