@@ -428,11 +428,13 @@ def main():
         # kd_fa_run_ws: the mask summary pass, then the short-key kernel,
         # which skips the fully masked key tiles of each 32-row block without
         # loading their mask rows; kd_fa_run (no workspace) beside it
-        # (10 warmup calls: the first calls after the buffers are allocated
-        # run up to 10% slower)
+        # (after the long self-attention runs above this GPU's clock recovers
+        # over tens of milliseconds: the two forms are timed alternately,
+        # twice each, and the second timing of each is reported)
         ws2m = torch.empty(max(kd_fa.workspace_size_full(d2), 16), dtype=torch.uint8, device=dev)
-        ms2n = time_launches(torch, lambda: kd_fa.run_desc(d2, None, stream), 50, 10, stream)
-        ms2 = time_launches(torch, lambda: kd_fa.run_desc(d2, None, stream, ws2m), 50, 10, stream)
+        for _ in range(2):
+            ms2n = time_launches(torch, lambda: kd_fa.run_desc(d2, None, stream), 50, 10, stream)
+            ms2 = time_launches(torch, lambda: kd_fa.run_desc(d2, None, stream, ws2m), 50, 10, stream)
         bytes2 = (q.numel() + k2.numel() + v2.numel()) * 2 + m2.numel() * 2 + out2.numel() * 4
         sec["cross_attn_ms"] = round(ms2, 4)
         sec["cross_attn_GBps"] = round(bytes2 / (ms2 * 1e-3) / 1e9, 1)
