@@ -20,6 +20,8 @@ and the allocation-free entry point take the summary too; the production
 shape closes the file.
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -220,3 +222,27 @@ def test_summary_production_cross_attention():
     rows = sample_rows(B, H, L, 16, seed=3)
     ref = orc.fa_f64(q.cpu(), k.cpu(), v.cpu(), mask=m.cpu(), scale=D ** -0.5, rows=rows)
     assert_parity(gather_rows(dst_ws, rows, H, L), ref, "mask summary production")
+
+
+def test_small_or_missing_workspace_is_kd_fa_run():
+    """kd_fa_run_ws with a workspace below kd_fa_workspace_size, or none,
+    runs as kd_fa_run (bitwise); an unmasked node uses no workspace."""
+    _need_gpu()
+    B, H, Lq, Lk = 2, 2, 130, 200
+    _announce("mask summary: small / missing workspace")
+    q, k, v = qkv(B, H, Lq, Lk, torch.bfloat16, seed=21)
+    m = _mask("stair", B, H, Lq, Lk, seed=3)[:, :, :Lq, :].to(DEV)
+    q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+    outs = [torch.empty((B, Lq, H, D), dtype=torch.float32, device=DEV) for _ in range(3)]
+    descs = [kd_fa.make_desc(q, k, v, m, o, D ** -0.5) for o in outs]
+    need = kd_fa.workspace_size_full(descs[0])
+    small = _garbage_ws(need - 16)
+    assert kd_fa.run_desc(descs[0]) == kd_fa.OK
+    assert kd_fa.run_desc(descs[1], workspace=small) == kd_fa.OK
+    lib = kd_fa.lib()
+    h = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.kd_fa_run_ws(ctypes.byref(descs[2]), None, 0, h) == kd_fa.OK
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    nm = kd_fa.make_desc(q, k, v, None, outs[0], D ** -0.5)
+    assert kd_fa.workspace_size_full(nm) == 0
