@@ -207,3 +207,21 @@ def test_d512_key_split(case):
     rows = np.arange(B * H * Lq) if Lq <= 1024 else sample_rows(B, H, Lq, 64, seed=5)
     ref = orc.fa_f64(q.cpu(), k.cpu(), v.cpu(), scale=scale, rows=rows)
     assert_parity(gather_rows(outs[0].float(), rows, H, Lq), ref, f"d512 key split {case}")
+
+
+def test_d512_key_split_in_static_scratch():
+    """kd_fa_dit_run_static on the VAE node keeps the key split's partial
+    results in the library's static scratch: bitwise kd_fa_run_ws with a
+    caller workspace."""
+    _need_gpu()
+    _announce("d512 key split in the static scratch")
+    L = 2048
+    q, k, v = _qkv(1, 1, L, L, torch.float16, seed=51)
+    q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+    outs = [torch.empty((1, L, 1, D), dtype=torch.float32, device=DEV) for _ in range(2)]
+    descs = [kd_fa.make_desc(q, k, v, None, o, D ** -0.5) for o in outs]
+    ws = torch.empty(kd_fa.workspace_size_full(descs[0]), dtype=torch.uint8, device=DEV)
+    assert kd_fa.run_desc(descs[0], workspace=ws) == kd_fa.OK
+    assert kd_fa.run_static(descs[1]) == kd_fa.OK
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
