@@ -306,8 +306,11 @@ int kd_fa_rope_text_table(int L, int D, float theta, float *out);
  * GPU, held until the process ends) is set up on the first call on each
  * device.  A node whose transformed K (the kd_fa_rope_workspace_size bytes)
  * exceeds the array is refused with KD_FA_ERR_SCRATCH before any device
- * work; a node that transforms no K needs no workspace and always runs.
- * The result is bitwise equal to kd_fa_dit_run's with a caller workspace.
+ * work; a node that transforms no K needs no K workspace and always runs.
+ * The array also holds what kd_fa_workspace_size counts beyond K (the mask
+ * summary, the D = 512 key split's partial results) when that fits; else
+ * the call runs without it.  The result is bitwise equal to kd_fa_dit_run's
+ * with a caller workspace of the same size.
  * Every call on a GPU shares that GPU's array: calls that overlap on one
  * GPU (two streams, two host threads) race and must be serialised by the
  * caller.
