@@ -9,7 +9,11 @@ kernel out, with the short-key kernel out, with the 64-row kernel taking the
 short unmasked key sets too, and with both specialised kernels out.  Every
 kernel computes each query row with the same arithmetic, so all outputs must
 be bitwise equal; the routed one must also match the float64 oracle on every
-row.  The cases are fixed by their seeds (no draw differs between runs).
+row.  Odd seeds give the mask rows whole 8-key chunks (ggml pads them; the
+values past Lk must not count), which lets masked key sets of up to 256 keys
+reach the short-key kernel, and every case also runs kd_fa_run_ws (the mask
+summary), which must give the same bits.  The cases are fixed by their seeds
+(no draw differs between runs).
 """
 import numpy as np
 import pytest
@@ -50,17 +54,19 @@ def _case(seed):
     return B, Bk, H, Hkv, Lq, Lk, kv, qt, mask, scale
 
 
-def _mask(kind, B, Lq, Lk, seed):
+def _mask(kind, B, Lq, Lk, seed, ne0=None):
     if kind == "none":
         return None
+    ne0 = Lk if ne0 is None else ne0
     g = torch.Generator().manual_seed(seed)
     if kind == "pad":
-        m = torch.full((B, 1, Lq, Lk), float("-inf"), dtype=torch.float16)
+        m = torch.full((B, 1, Lq, ne0), float("-inf"), dtype=torch.float16)
         for b in range(B):
             m[b, :, :, : int(torch.randint(1, Lk + 1, (1,), generator=g))] = 0.0
-        return m
-    m = (torch.randn((B, 1, Lq, Lk), generator=g) * 2).to(torch.float16)
-    m[torch.rand((B, 1, Lq, Lk), generator=g) < 0.3] = float("-inf")
+    else:
+        m = (torch.randn((B, 1, Lq, ne0), generator=g) * 2).to(torch.float16)
+        m[torch.rand((B, 1, Lq, ne0), generator=g) < 0.3] = float("-inf")
+    m[..., Lk:] = 3.0       # padding past Lk: never read as a key
     return m
 
 
@@ -73,16 +79,22 @@ def test_random_shape_all_routes_bitwise_and_oracle(seed):
     q = randn((B, H, Lq, D), qt, 50 + seed)
     k = randn((Bk, Hkv, Lk, D), kv, 150 + seed)
     v = randn((Bk, Hkv, Lk, D), kv, 250 + seed)
-    mask = _mask(mk, B, Lq, Lk, 350 + seed)
+    mask = _mask(mk, B, Lq, Lk, 350 + seed, ne0=(Lk + 7) // 8 * 8 if seed % 2 else None)
     qg, kg, vg = q.to(DEV), k.to(DEV), v.to(DEV)
     mg = None if mask is None else mask.to(DEV)
     outs = []
     for route in ROUTES:
         with kd_fa.routing(route):
             outs.append(kd_fa.flash_attn_ext(qg, kg, vg, mask=mg, scale=scale))
+    # kd_fa_run_ws: the mask summary where the short-key kernel runs
+    out_ws = torch.empty_like(outs[0])
+    d = kd_fa.make_desc(qg, kg, vg, mg, out_ws, scale)
+    ws = torch.empty(max(kd_fa.workspace_size_full(d), 16), dtype=torch.uint8, device=DEV).fill_(0x5A)
+    assert kd_fa.run_desc(d, workspace=ws) == kd_fa.OK
     torch.cuda.synchronize()
     for route, out in zip(ROUTES[1:], outs[1:]):
         assert torch.equal(out, outs[0]), f"{what}: route {route} differs from the routed output"
+    assert torch.equal(out_ws, outs[0]), f"{what}: kd_fa_run_ws differs from kd_fa_run"
     ref = orc.fa_f64(q, k, v, mask=mask, scale=scale)
     got = gather_rows(outs[0], np.arange(B * H * Lq), H, Lq)
     assert_parity(got, ref, what)
