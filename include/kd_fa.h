@@ -156,7 +156,8 @@ int kd_fa_run(const kd_fa_desc *desc, void *stream);
  * kernels take scratch from the backend's buffer pool while the node runs
  * (ggml_backend_graph_compute, src/core/executor.hpp:241): a masked node
  * whose key set is short (Lk <= 256: the text cross-attention,
- * src/models/crossdit.hpp:174-200) keeps in it a summary of which 64-key
+ * src/models/crossdit.hpp:174-200) with at least 65,536 query rows in all
+ * (Lq * H * B) keeps in it a summary of which 64-key
  * tiles of its mask hold finite values for each 32-row block of queries,
  * written by a pass over the mask on `stream`, so that the attention skips
  * the fully masked tiles of a block without loading their mask rows; the
@@ -335,8 +336,10 @@ enum {
     KD_FA_ROUTE_D512_R1 = 4,   /* D = 512: one 32-row block per workgroup                 */
     KD_FA_ROUTE_NO_SPLIT = 8,  /* D = 512, short query sets: no key split (one pass)     */
     KD_FA_ROUTE_W64_SHORT = 16, /* unmasked key sets <= 896 too: the 64-row kernel       */
-    KD_FA_ROUTE_STAGED = 32     /* K transformed without a workspace: staged whenever the
+    KD_FA_ROUTE_STAGED = 32,    /* K transformed without a workspace: staged whenever the
                                    shape allows, also where one on-load launch is cheaper */
+    KD_FA_ROUTE_SUMMARY = 64    /* mask summary for every masked short-key node with the
+                                   workspace, also below 65,536 query rows             */
 };
 int kd_fa_set_routing(int flags);
 

@@ -191,6 +191,13 @@ D512Split d512_split(int64_t Lq, int64_t Lk, int64_t H, int64_t B, int route) {
 size_t summary_offset(const kd_fa_desc *d, bool k_xform) {
     return k_xform ? (rope_ws_bytes(d) + 255) / 256 * 256 : 0;
 }
+// The summary pass costs a launch and one read of the mask (~9 us at the
+// 31,744-token cross-attention, whose kernel it shortens by ~33 us); below
+// 65,536 query rows in all (2,048 tokens x 32 heads) the launch is not paid
+// back, and the call runs without it.  KD_FA_ROUTE_SUMMARY builds it for every
+// masked short-key node that has the workspace (for comparisons).
+bool summary_pays(int64_t rows, int route) { return (route & KD_FA_ROUTE_SUMMARY) || rows >= 65536; }
+
 size_t summary_bytes(const kd_fa_desc *d, bool rope_on) {
     if (!d->mask.data || rope_on || d->q.ne[0] != kHeadDim || d->k.ne[1] > kdfa::kXresMaxKeys) return 0;
     return 4 * (size_t)d->mask.ne[3] * (size_t)d->mask.ne[2] * (size_t)((d->q.ne[1] + 31) / 32);
@@ -512,7 +519,7 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
         // for all rows of a block are then skipped without loading their
         // mask chunks (one L2 round trip per dead tile and block)
         const size_t s_off = summary_offset(d, k_xform), s_bytes = summary_bytes(d, rope_on);
-        if (a.m && ws && s_bytes && ws_bytes >= s_off + s_bytes) {
+        if (a.m && ws && s_bytes && ws_bytes >= s_off + s_bytes && summary_pays(Lq * H * B, route)) {
             uint32_t *sum = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + s_off);
             if (kdfa::launch_mask_live(a, sum, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
             a.m_live = sum;

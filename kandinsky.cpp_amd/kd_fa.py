@@ -60,6 +60,7 @@ ROUTE_D512_R1 = 4
 ROUTE_NO_SPLIT = 8
 ROUTE_W64_SHORT = 16
 ROUTE_STAGED = 32
+ROUTE_SUMMARY = 64
 
 
 class KdFaTensor(ctypes.Structure):

@@ -17,7 +17,10 @@ broadcast over batches, ragged key counts (a partial last tile) and ragged
 query counts (the last block's rows past Lq read row Lq - 1).  The query /
 key RMSNorm path (K transformed into the workspace, the summary after it)
 and the allocation-free entry point take the summary too; the production
-shape closes the file.
+shape closes the file.  Below 65,536 query rows in all the library skips the
+pass (its launch would not pay back); the small cases here build it with
+KD_FA_ROUTE_SUMMARY, and one case checks that the default leaves the
+workspace untouched there.
 """
 
 import ctypes
@@ -142,7 +145,8 @@ def test_summary_skips_dead_tiles_bitwise(case):
     assert need == 4 * Bm * Hm * ((Lq + 31) // 32)
     ws = _garbage_ws(need)
     assert kd_fa.run_desc(d) == kd_fa.OK
-    assert kd_fa.run_desc(d_ws, workspace=ws) == kd_fa.OK
+    with kd_fa.routing(kd_fa.ROUTE_SUMMARY):
+        assert kd_fa.run_desc(d_ws, workspace=ws) == kd_fa.OK
     torch.cuda.synchronize()
     words = ws[:need].cpu().numpy().view(np.uint32)
     ref_words = _summary_ref(mv, Lq, Lk)
@@ -160,7 +164,8 @@ def test_summary_parity_against_oracle():
     dst = torch.empty((B, Lq, H, D), dtype=torch.float32, device=DEV)
     d = kd_fa.make_desc(q.to(DEV), k.to(DEV), v.to(DEV), m.to(DEV), dst, D ** -0.5)
     ws = _garbage_ws(kd_fa.workspace_size_full(d))
-    assert kd_fa.run_desc(d, workspace=ws) == kd_fa.OK
+    with kd_fa.routing(kd_fa.ROUTE_SUMMARY):
+        assert kd_fa.run_desc(d, workspace=ws) == kd_fa.OK
     torch.cuda.synchronize()
     ref = orc.fa_f64(q, k, v, mask=m, scale=D ** -0.5)
     assert_parity(gather_rows(dst, np.arange(B * H * Lq), H, Lq), ref, "mask summary")
@@ -186,10 +191,11 @@ def test_summary_after_transformed_k_and_static_entry():
     kbytes = kd_fa.workspace_size(descs[0])
     assert full == (kbytes + 255) // 256 * 256 + 4 * 2 * ((Lq + 31) // 32)
     ws_full, ws_k = _garbage_ws(full), _garbage_ws(kbytes)
-    assert kd_fa.run_desc(descs[0], None, None, ws_full, norm) == kd_fa.OK
-    assert kd_fa.run_desc(descs[1], None, None, ws_k, norm) == kd_fa.OK
-    assert kd_fa.run_desc(descs[2], None, None, None, norm) == kd_fa.OK
-    assert kd_fa.run_static(descs[3], None, norm) == kd_fa.OK
+    with kd_fa.routing(kd_fa.ROUTE_SUMMARY):
+        assert kd_fa.run_desc(descs[0], None, None, ws_full, norm) == kd_fa.OK
+        assert kd_fa.run_desc(descs[1], None, None, ws_k, norm) == kd_fa.OK
+        assert kd_fa.run_desc(descs[2], None, None, None, norm) == kd_fa.OK
+        assert kd_fa.run_static(descs[3], None, norm) == kd_fa.OK
     torch.cuda.synchronize()
     words = ws_full[(kbytes + 255) // 256 * 256: full].cpu().numpy().view(np.uint32)
     assert np.array_equal(words, _summary_ref(m.cpu(), Lq, Lk))
@@ -246,3 +252,27 @@ def test_small_or_missing_workspace_is_kd_fa_run():
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
     nm = kd_fa.make_desc(q, k, v, None, outs[0], D ** -0.5)
     assert kd_fa.workspace_size_full(nm) == 0
+
+
+def test_summary_skipped_below_the_row_threshold():
+    """Below 65,536 query rows the default route runs without the summary
+    (the workspace is left as it was); KD_FA_ROUTE_SUMMARY builds it; both
+    give kd_fa_run's bits."""
+    _need_gpu()
+    B, H, Lq, Lk = 1, 2, 200, 256
+    _announce("mask summary threshold")
+    q, k, v = qkv(B, H, Lq, Lk, torch.bfloat16, seed=31)
+    m = _mask("stair", B, H, Lq, Lk, seed=4)[:, :, :Lq, :].to(DEV)
+    q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+    outs = [torch.empty((B, Lq, H, D), dtype=torch.float32, device=DEV) for _ in range(3)]
+    descs = [kd_fa.make_desc(q, k, v, m, o, D ** -0.5) for o in outs]
+    need = kd_fa.workspace_size_full(descs[0])
+    ws_a, ws_b = _garbage_ws(need), _garbage_ws(need)
+    assert kd_fa.run_desc(descs[0]) == kd_fa.OK
+    assert kd_fa.run_desc(descs[1], workspace=ws_a) == kd_fa.OK
+    with kd_fa.routing(kd_fa.ROUTE_SUMMARY):
+        assert kd_fa.run_desc(descs[2], workspace=ws_b) == kd_fa.OK
+    torch.cuda.synchronize()
+    assert torch.all(ws_a[:need] == 0xA5)
+    assert np.array_equal(ws_b[:need].cpu().numpy().view(np.uint32), _summary_ref(m.cpu(), Lq, Lk))
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
