@@ -90,7 +90,7 @@ def time_launches(torch, fn, steps, warmup, stream):
 
 
 def cpu_share():
-    """Host threads a one-GPU job may use: OMP_NUM_THREADS (the GPU box's
+    """Host threads a one-GPU job may use: OMP_NUM_THREADS (the host's CPU
     share for one GPU), else the CPUs this process may run on."""
     try:
         n = int(os.environ.get("OMP_NUM_THREADS", "0"))
@@ -248,7 +248,7 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the attention node runs on a single MI355X "
-              "(multi-GPU sharding is a design note, not part of this build)", file=sys.stderr)
+              "(multi-GPU sharding is a design note, not implemented)", file=sys.stderr)
         sys.exit(2)
 
     import torch

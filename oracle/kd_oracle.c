@@ -1,8 +1,8 @@
 /*
  * kd_oracle.c - CPU oracle for the CrossDiT flash-attention hot path.
  *
- * TEST INFRASTRUCTURE ONLY (the checker, never the thing measured or
- * shipped).  Loaded by tests/, __graft_entry__.smoke() and the
+ * TEST INFRASTRUCTURE ONLY (what results are checked against, never the
+ * thing measured or shipped).  Loaded by tests/, __graft_entry__.smoke() and the
  * cpu_baseline leg of bench.py; the product library never links it.
  *
  * Built with -ffp-contract=off so that every a*b+c written below rounds

@@ -1,7 +1,7 @@
 /*
  * kd_oracle.h - CPU oracle for the CrossDiT flash-attention hot path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker: only the test
+ * TEST INFRASTRUCTURE ONLY.  Results are checked against this library: only the test
  * suite, the smoke check and the CPU-baseline leg of the benchmark load it.
  * The product library (libkd_fa.so) never links or calls it.
  *

@@ -1,6 +1,6 @@
 """ctypes binding of oracle/libkd_oracle.so.
 
-TEST INFRASTRUCTURE ONLY: the checker.  Imported by tests/, by
+TEST INFRASTRUCTURE ONLY: results are checked against it.  Imported by tests/, by
 __graft_entry__.smoke() and by bench.py's cpu_baseline leg, never by the
 product (kandinsky.cpp_amd/).
 

@@ -1,7 +1,7 @@
 """CPU restatement of the linear-layer path: the weight block formats and the
 GGML_OP_MUL_MAT arithmetic of ops::linear (src/core/ops.hpp:27-43).
 
-TEST INFRASTRUCTURE ONLY: the checker.  Imported by tests/, never by the
+TEST INFRASTRUCTURE ONLY: results are checked against it.  Imported by tests/, never by the
 product (kandinsky.cpp_amd/).
 
 Sources restated (numpy, vectorised):
