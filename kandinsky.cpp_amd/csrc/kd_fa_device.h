@@ -186,6 +186,22 @@ static __device__ __forceinline__ float max32(const float *p) {
     return max3(x, y, __builtin_fmaxf(p[30], p[31]));
 }
 
+// max32 for scores fresh from the matrix unit: max3 is inline asm, whose
+// operands the compiler does not check against the wait states that an MFMA
+// result needs before a vector instruction reads it; these v_max it sees.
+// The same value as max32 (a max is exact; either zero may stand for a
+// +-0 tie, which gives every weight and rescale factor the same value).
+static __device__ __forceinline__ float max32_mfma(const float *p) {
+    float x = __builtin_fmaxf(p[0], p[1]);
+    float y = __builtin_fmaxf(p[2], p[3]);
+#pragma unroll
+    for (int i = 4; i < 32; i += 4) {
+        x = __builtin_fmaxf(x, __builtin_fmaxf(p[i], p[i + 1]));
+        y = __builtin_fmaxf(y, __builtin_fmaxf(p[i + 2], p[i + 3]));
+    }
+    return __builtin_fmaxf(x, y);
+}
+
 // max over the lane pair (l, l ^ 32) that shares one query row
 static __device__ __forceinline__ float pair_max(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);

@@ -1026,6 +1026,10 @@ void fa_fwd_xres(Args a) {
 
     f32x16 o[4];
     float m_run, l_half;
+    // true until the block's first PV: O and l_half are still 0 in every
+    // row, so moving the running max needs no rescale (0 * alpha = 0 for
+    // the alpha in [0, 1] it would apply).  Wave-uniform.
+    bool o_zero;
     // the block's live key tiles (bit t: tile t holds a finite mask value
     // for one of its rows), from the mask summary when the call has one,
     // else every tile (each is then checked on its mask chunks); the mask
@@ -1062,13 +1066,17 @@ void fa_fwd_xres(Args a) {
     auto move_max = [&](float mx, bool up) __attribute__((always_inline)) {   // fa_fwd_d128's rules, per row
         if (__builtin_amdgcn_ballot_w64(up) != 0) {
             const float m_new = up ? __builtin_fmaxf(m_run, mx) : m_run;
-            const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-            m_run = m_new;
-            l_half *= alpha;
+            if (o_zero) {
+                m_run = m_new;
+            } else {
+                const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+                m_run = m_new;
+                l_half *= alpha;
 #pragma unroll
-            for (int dblk = 0; dblk < 4; ++dblk)
+                for (int dblk = 0; dblk < 4; ++dblk)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) o[dblk][i] *= alpha;
+                    for (int i = 0; i < 16; ++i) o[dblk][i] *= alpha;
+            }
         }
     };
     auto update_max = [&](float mx) __attribute__((always_inline)) { move_max(mx, mx > m_run + kTau); };
@@ -1153,6 +1161,7 @@ void fa_fwd_xres(Args a) {
         vec8 pb[4];
         l_half += pack_sum(p, pb);
         pv(sV + t * kTileBytes, pb);
+        o_zero = false;
     };
     // unmasked tile: weights against the current running max, the exact max
     // and a redo only when a row's weight sum leaves [0, E::kSumCap]; keys past
@@ -1173,6 +1182,15 @@ void fa_fwd_xres(Args a) {
         };
         vec8 pb[4];
         float p[32];
+        if (o_zero) {
+            // the block's first tile: every row's running max is -inf, so
+            // its weights would all be +inf, leave [0, cap] and take the
+            // exact max below; take it here, before the one pass of exp2
+            float q[32];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) { q[i] = s0[i]; q[16 + i] = s1[i]; }
+            move_max(pair_max(max32_mfma(q)) * c2, true);
+        }
         float nm = -m_run;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -1198,6 +1216,7 @@ void fa_fwd_xres(Args a) {
         }
         l_half += sum;
         pv(sV + t * kTileBytes, pb);
+        o_zero = false;
     };
 
     if constexpr (!HAS_MASK) load_uniforms(&a);
@@ -1235,6 +1254,7 @@ void fa_fwd_xres(Args a) {
         for (int i = 0; i < 4; ++i) o[i] = (f32x16){};
         m_run = -INFINITY;
         l_half = 0.0f;
+        o_zero = true;
 #pragma unroll
         for (int t = 0; t < kXNT; ++t) {
             if (t < n_tiles && ((live >> t) & 1u)) {
