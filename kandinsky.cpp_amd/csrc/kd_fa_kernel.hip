@@ -581,7 +581,7 @@ void fa_fwd_d128(Args a) {
             float q[32];
 #pragma unroll
             for (int i = 0; i < 16; ++i) { q[i] = s0[i]; q[16 + i] = s1[i]; }
-            move_max(pair_max(max32(q)) * c2, !(pair <= E::kSumCap));
+            move_max(pair_max(max32_mfma(q)) * c2, !(pair <= E::kSumCap));
             nm = -m_run;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
@@ -670,7 +670,7 @@ void fa_fwd_d128(Args a) {
                 float q[32];
 #pragma unroll
                 for (int i = 0; i < 16; ++i) { q[i] = c0[i]; q[16 + i] = c1[i]; }
-                move_max(pair_max(max32(q)) * c2, !(pair <= E::kSumCap));
+                move_max(pair_max(max32_mfma(q)) * c2, !(pair <= E::kSumCap));
                 nm = -m_run;
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
@@ -1204,7 +1204,7 @@ void fa_fwd_xres(Args a) {
             float q[32];
 #pragma unroll
             for (int i = 0; i < 16; ++i) { q[i] = s0[i]; q[16 + i] = s1[i]; }
-            move_max(pair_max(max32(q)) * c2, !(pair <= E::kSumCap));
+            move_max(pair_max(max32_mfma(q)) * c2, !(pair <= E::kSumCap));
             nm = -m_run;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
