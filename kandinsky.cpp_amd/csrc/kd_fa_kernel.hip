@@ -613,6 +613,15 @@ void fa_fwd_d128(Args a) {
         f32x16 sa0, sa1, sb0, sb1;
         if (n_tiles > 0) qk(sK0, sa0, sa1);
         __syncthreads();   // every wave is done with K(0) before K(2) lands in its buffer
+        if (n_tiles > 0) {
+            // step 0 against m_run = -inf would give every weight +inf and
+            // redo the step against its exact max: take that max here (O
+            // and the row sums are still 0: nothing to rescale)
+            float q[32];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) { q[i] = sa0[i]; q[16 + i] = sa1[i]; }
+            m_run = __builtin_fmaxf(m_run, pair_max(max32_mfma(q)) * c2);
+        }
         // c0, c1: scores of tile t; n0, n1 <- scores of tile t+1 (NEXT)
         auto pstep = [&](auto next_c, auto tail_c, int t, const f32x16 &c0, const f32x16 &c1, f32x16 &n0,
                          f32x16 &n1, const lds_t *kn_, const lds_t *vs_, lds_t *dK, lds_t *dV)
