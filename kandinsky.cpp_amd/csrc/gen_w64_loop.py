@@ -451,6 +451,28 @@ class Gen:
         blk += ["s_nop 7", f"s_branch {back}"]
         self.slow.append(blk)
 
+    @staticmethod
+    def row_max(e, p, qb, w):
+        """X = the exact row max of S[p][qb] over the lane pair, times |c2|
+        (w: three temporaries)."""
+        sb = S_BASE[p] + 32 * qb
+        s = [vr(sb + i) for i in range(32)]
+        e(valu(f"v_max3_f32 {vr(w[0])}, {s[0]}, {s[1]}, {s[2]}", set(s[0:3]), {vr(w[0])}))
+        e(valu(f"v_max3_f32 {vr(w[1])}, {s[3]}, {s[4]}, {s[5]}", set(s[3:6]), {vr(w[1])}))
+        for i in range(6, 30, 4):
+            e(valu(f"v_max3_f32 {vr(w[0])}, {vr(w[0])}, {s[i]}, {s[i + 1]}", {vr(w[0]), s[i], s[i + 1]}, {vr(w[0])}))
+            e(valu(f"v_max3_f32 {vr(w[1])}, {vr(w[1])}, {s[i + 2]}, {s[i + 3]}", {vr(w[1]), s[i + 2], s[i + 3]},
+                   {vr(w[1])}))
+        e(valu(f"v_max_f32 {vr(w[2])}, {s[30]}, {s[31]}", {s[30], s[31]}, {vr(w[2])}))
+        e(valu(f"v_max3_f32 {vr(w[0])}, {vr(w[0])}, {vr(w[1])}, {vr(w[2])}", {vr(w[0]), vr(w[1]), vr(w[2])},
+               {vr(w[0])}))
+        # max over the lane pair, times |c2|
+        e(valu(f"v_mov_b32 {vr(X)}, {vr(w[0])}", {vr(w[0])}, {vr(X)}))
+        e(valu(f"v_mov_b32 {vr(Y)}, {vr(w[0])}", {vr(w[0])}, {vr(Y)}))
+        e(Ins(f"v_permlane32_swap_b32 {vr(X)}, {vr(Y)}", "perm", {vr(X), vr(Y)}, {vr(X), vr(Y)}))
+        e(valu(f"v_max_f32 {vr(X)}, {vr(X)}, {vr(Y)}", {vr(X), vr(Y)}, {vr(X)}))
+        e(valu(f"v_mul_f32 {vr(X)}, |%[c2]|, {vr(X)}", {vr(X)}, {vr(X)}))
+
     def slow_block(self, p, qb, tag):
         """Exact row max of S[p][qb]; the rows whose own weight sum failed
         the check move to it, with O and the sums rescaled; all 32 weights
@@ -619,6 +641,13 @@ class Gen:
             e(r)
         self.merge(tr, seq, [])
         tr.raw("s_barrier")
+        # step 0's exact row max: against the running max of -inf every
+        # weight of S(0) would be +inf, fail step 0's check and be redone on
+        # the slow path against this max (O and the sums, still 0, need no
+        # rescale); max(-inf, X) as the slow path's move gives it
+        for qb in range(2):
+            self.row_max(e, 0, qb, [W_BASE + i for i in range(3)])
+            e(valu(f"v_max_f32 {vr(M[qb])}, {vr(M[qb])}, {vr(X)}", {vr(M[qb]), vr(X)}, {vr(M[qb])}))
         for x in self.softmax_half(0, 0, 0, (0, 1), True):
             e(x)
         # steps: pairs while t + 2 < n, then one or two more
