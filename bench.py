@@ -53,8 +53,8 @@ def parse():
     p.add_argument("--cross-only", action="store_true",
                    help="only the text cross-attention (C2 shape): for counter runs of its kernel")
     p.add_argument("--hbm-ceiling", action="store_true",
-                   help="only the HBM streaming probes (libkd_probe.so) at the cross-attention's sizes: "
-                        "bf16 -> F32 widening (its Q-in / O-out byte mix), read-only, write-only")
+                   help="only torch's bf16 -> F32 copy at the cross-attention's sizes (its Q-in / O-out "
+                        "byte mix) and a 1 GiB F32 copy")
     return p.parse_args()
 
 
@@ -160,7 +160,8 @@ def cpu_baseline(torch, dev, q3, k3, v3, table3, rows3, rows4):
     del q4, k4, v4
     return {"value": round(c3, 6), "unit": "TFLOP/s", "cores": used, "host_cores": os.cpu_count(),
             "kind": "port",
-            "sample": (f"ggml per-row CPU flash-attn algorithm (restated, oracle/kd_oracle.c) on {used} threads "
+            "sample": (f"ggml per-row CPU flash-attn algorithm (restated, oracle/kd_oracle.c; F16 V accumulator "
+                       f"converted by F16C as ggml's SIMD path does) on {used} threads "
                        f"(the CPU share of a one-GPU job; {os.cpu_count()} cores on the host): value = the "
                        f"31,744-token self-attention with RoPE on {rows3} query rows per (b,h) x {B * HEADS} "
                        f"heads, all keys ({dt3:.2f} s wall); the 1,280-token self-attention and the text "
@@ -175,6 +176,41 @@ def rope_rows_f32(torch, x, c, s):
     o0 = x0 * c - x1 * s
     o1 = x0 * s + x1 * c
     return torch.stack((o0, o1), dim=-1).flatten(-2)
+
+
+def lazy_cap_steps(torch, q, k, table, cap, waves=16, seed=5):
+    """How often the 64-row kernel's lazy row max leaves its fast path on
+    these operands: for `waves` sampled waves (64 consecutive query rows of
+    one (b, h)), the logits in the log2 domain from the rotated operands
+    rounded to K's type, then the kernel's rule per row -- the running max is
+    the first tile's exact max; a later 64-key tile whose weight sum
+    exp2(s - m) leaves [0, cap] moves m to that tile's max -- and a wave's
+    step is slow when any of its rows moves.  Returns the fraction of the
+    steps after the first that are slow (a model, in float64 on the GPU)."""
+    B, H, L, Dh = q.shape
+    tab = torch.from_numpy(table).to(q.device)
+    c, s = tab[:, 0::2], tab[:, 1::2]
+    g = torch.Generator().manual_seed(seed)
+    scale = math.log2(math.e) / math.sqrt(Dh)
+    slow, total = 0, 0
+    for _ in range(waves):
+        b = int(torch.randint(0, B, (1,), generator=g))
+        h = int(torch.randint(0, H, (1,), generator=g))
+        r0 = int(torch.randint(0, L // 64, (1,), generator=g)) * 64
+        kr = rope_rows_f32(torch, k[b, h].float(), c, s).to(k.dtype).double()
+        qr = rope_rows_f32(torch, q[b, h, r0:r0 + 64].float(), c[r0:r0 + 64], s[r0:r0 + 64]).to(k.dtype).double()
+        sc = (qr @ kr.T) * scale                              # (64, L) log2 domain
+        n_t = (L + 63) // 64
+        m = sc[:, :64].max(dim=1).values
+        for t in range(1, n_t):
+            st = sc[:, 64 * t:64 * t + 64]
+            tot = torch.exp2(st - m[:, None]).sum(dim=1)
+            move = ~(tot <= cap)
+            if bool(move.any()):
+                slow += 1
+                m = torch.where(move, torch.maximum(m, st.max(dim=1).values), m)
+            total += 1
+    return round(slow / max(total, 1), 6)
 
 
 def self_check(torch, q, k, v, table, out, scale, rows_per_head=4, seed=11):
@@ -206,41 +242,21 @@ def self_check(torch, q, k, v, table, out, scale, rows_per_head=4, seed=11):
 
 
 def hbm_ceiling(torch, dev, stream):
-    """What this GPU sustains for the cross-attention's byte mix: a bf16 array
-    of the C2 query size (520 MB) widened to F32 (1.04 GB written), read-only
-    and write-only streams of the same arrays; best over launch sizes, the
-    mean of 20 launches each (HIP events on the launch stream)."""
-    import ctypes
-    lib = ctypes.CDLL(os.path.join(ROOT, "kandinsky.cpp_amd", "libkd_probe.so"))
-    lib.kd_probe_widen.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
-                                   ctypes.c_void_p]
-    lib.kd_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
-    lib.kd_probe_write.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+    """What this GPU sustains for the cross-attention's byte mix: torch's own
+    copy of a bf16 array of the C2 query size (520 MB) into an F32 array
+    (1.04 GB written), and a 1 GiB F32 device copy; the mean of 20 launches
+    each (HIP events on the launch stream)."""
     n = 2 * HEADS * 31744 * D
     src = torch.ones(n, dtype=torch.bfloat16, device=dev)
     dst = torch.empty(n, dtype=torch.float32, device=dev)
-    sink = torch.empty(65536 * 4, dtype=torch.int32, device=dev)
-    h = ctypes.c_void_p(stream.cuda_stream)
-    n16 = n * 2 // 16
     res = {"bytes_read": n * 2, "bytes_written": n * 4}
-    widen = [(f"widen_bf16_to_f32_u{v % 10}{'_nt' if v > 10 else ''}",
-              (lambda v: lambda g: lib.kd_probe_widen(src.data_ptr(), dst.data_ptr(), n16, g, v, h))(v), n * 6)
-             for v in (1, 4, 8, 11, 14, 18)]
-    for name, fn, nbytes in widen + [
-            ("read", lambda g: lib.kd_probe_read(dst.data_ptr(), sink.data_ptr(), n * 4 // 16, g, h), n * 4),
-            ("write", lambda g: lib.kd_probe_write(dst.data_ptr(), n * 4 // 16, g, h), n * 4)]:
-        best = None
-        for g in (1024, 2048, 4096, 8192, 16384):
-            ms = time_launches(torch, lambda: fn(g), 20, 3, stream)
-            gbs = nbytes / (ms * 1e-3) / 1e9
-            if best is None or gbs > best[1]:
-                best = (g, gbs, ms)
-        res[name] = {"GBps": round(best[1], 1), "ms": round(best[2], 4), "blocks": best[0],
-                     "frac_of_8TBps": round(best[1] / PEAK_HBM_GBS, 4)}
-    # torch's own widening copy for comparison
-    dv = dst.view(-1)
-    ms = time_launches(torch, lambda: dv.copy_(src), 20, 3, stream)
-    res["torch_copy_bf16_to_f32"] = {"GBps": round(n * 6 / (ms * 1e-3) / 1e9, 1), "ms": round(ms, 4)}
+    ms = time_launches(torch, lambda: dst.copy_(src), 20, 3, stream)
+    res["torch_copy_bf16_to_f32"] = {"GBps": round(n * 6 / (ms * 1e-3) / 1e9, 1), "ms": round(ms, 4),
+                                     "frac_of_8TBps": round(n * 6 / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+    a = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    ms = time_launches(torch, lambda: b.copy_(a), 20, 3, stream)
+    res["torch_copy_f32_1GiB"] = {"GBps": round(2 * a.numel() * 4 / (ms * 1e-3) / 1e9, 1), "ms": round(ms, 4)}
     return res
 
 
@@ -363,6 +379,40 @@ def main():
         sec["self_attn_fused_tflops"] = round(flop / (ms_f * 1e-3) / 1e12, 2)
         sec["self_attn_fused_note"] = ("kd_fa_rope_run, no workspace: K staged in output rows of later head "
                                        "groups, the last group rotating K on load")
+        # the reference's own operand form of this node (ops.hpp:122-169 via
+        # crossdit.hpp:150): Q F32, K/V F16 after ggml_cast, RoPE table, through
+        # kd_fa_rope_run_ws; on N(0,1) data and with peaked logits (Q and K
+        # scaled by 2: logit std 4), where the F16 sum cap (2^15) can send a
+        # wave's step to the exact-max slow path
+        for tag, sc in (("n01", 1.0), ("peaked_std4", 2.0)):
+            qf = rand(torch, (B, HEADS, L, D), 3, dev, torch.float32) * sc
+            kf = (rand(torch, (B, HEADS, L, D), 1003, dev, torch.float32) * sc).half()
+            vf = rand(torch, (B, HEADS, L, D), 2003, dev, torch.float16)
+            of = torch.empty((B, L, HEADS, D), device=dev, dtype=torch.float32)
+            dfx = kd_fa.make_desc(qf, kf, vf, None, of, 1.0 / D ** 0.5)
+            wsf = torch.empty(kd_fa.workspace_size(dfx), dtype=torch.uint8, device=dev)
+            msf = time_launches(torch, lambda: kd_fa.run_desc(dfx, rope, stream, wsf), 5, 1, stream)
+            sec[f"self_attn_refform_{tag}_ms"] = round(msf, 4)
+            sec[f"self_attn_refform_{tag}_tflops"] = round(flop / (msf * 1e-3) / 1e12, 2)
+            sec[f"self_attn_refform_{tag}_slow_steps"] = lazy_cap_steps(torch, qf, kf, table, 2.0 ** 15)
+            del qf, kf, vf, of, wsf
+        sec["self_attn_refform_note"] = ("Q F32 [128, 31744, 32, 2], K/V F16, RoPE table, kd_fa_rope_run_ws; "
+                                         "slow_steps: a model of the 64-row kernel's lazy max on 16 sampled "
+                                         "waves (64 rows x all keys each): fraction of 64-key steps after the "
+                                         "first in which a row's weight sum leaves [0, 2^15]")
+        # all three operands F32 (the node as ops::attention receives it,
+        # before its ggml_cast of K and V to F16): the pre-pass rotates and
+        # casts K and casts V into the workspace
+        q32, k32, v32 = (rand(torch, (B, HEADS, L, D), s_, dev, torch.float32) for s_ in (3, 1003, 2003))
+        o32 = torch.empty((B, L, HEADS, D), device=dev, dtype=torch.float32)
+        d32 = kd_fa.make_desc(q32, k32, v32, None, o32, 1.0 / D ** 0.5)
+        ws32 = torch.empty(kd_fa.workspace_size(d32), dtype=torch.uint8, device=dev)
+        ms32 = time_launches(torch, lambda: kd_fa.run_desc(d32, rope, stream, ws32), 5, 1, stream)
+        sec["self_attn_all_f32_ms"] = round(ms32, 4)
+        sec["self_attn_all_f32_tflops"] = round(flop / (ms32 * 1e-3) / 1e12, 2)
+        sec["self_attn_all_f32_note"] = ("Q/K/V F32 [128, 31744, 32, 2], RoPE table, kd_fa_rope_run_ws: one "
+                                         "pre-pass rotates and casts K and casts V to F16, then the attention")
+        del q32, k32, v32, o32, ws32
         # the attention alone on unrotated operands (kd_fa_run)
         ms_n = time_launches(torch, lambda: kd_fa.run_desc(desc, None, stream), args.steps, args.warmup, stream)
         sec["self_attn_norope_ms"] = round(ms_n, 4)
@@ -440,7 +490,7 @@ def main():
         sec["cross_attn_GBps"] = round(bytes2 / (ms2 * 1e-3) / 1e9, 1)
         sec["cross_attn_hbm_frac"] = round(bytes2 / (ms2 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
         sec["cross_attn_note"] = ("kd_fa_run_ws (mask summary in the workspace); "
-                                  "the measured ceiling for this byte mix is in profiles/hbm_ceiling_probes.txt")
+                                  "the measured ceiling for this byte mix: bench.py --hbm-ceiling")
         sec["cross_attn_no_ws_ms"] = round(ms2n, 4)
         # the reference's own cross-attention operand form (ops.hpp:122-169,
         # crossdit.hpp:198): Q F32, K/V F16, no mask, prompt lengths 77, 300

@@ -20,8 +20,9 @@
  *
  * Op contract (ggml GGML_OP_FLASH_ATTN_EXT, as ops.hpp:122-183 builds it):
  *   q    [Dk, Lq, H,   B ]  F32, F16 or BF16 (converted to K's type)
- *   k    [Dk, Lk, Hkv, Bk]  F16 or BF16
- *   v    [Dv, Lk, Hkv, Bk]  same type as k (not transposed)
+ *   k    [Dk, Lk, Hkv, Bk]  F16 or BF16 (F32 in the workspace forms)
+ *   v    [Dv, Lk, Hkv, Bk]  same type as k, not transposed (F32 in the
+ *                           workspace forms; see desc->cast_type)
  *   mask [Lk', Lq', Hm, Bm] F16, optional; Lk' >= Lk, Lq' >= Lq,
  *                           broadcast over heads (H % Hm == 0) and
  *                           batch (B % Bm == 0); row of query i is ne1 = i
@@ -38,6 +39,17 @@
  * All device pointers belong to the caller; no entry point allocates,
  * frees, synchronises or retains a pointer.  Work is enqueued on the given
  * HIP stream (NULL = the legacy default stream).
+ *
+ * dst must not overlap q, k, v, the mask, the RoPE table, the norm weights
+ * or the workspace: the kernels write output rows while other rows'
+ * operands are still being read, and without a workspace kd_fa_rope_run and
+ * kd_fa_dit_run also keep the transformed K of some heads in output rows of
+ * later heads during the call (those rows hold O when the call ends).
+ *
+ * ABI: the structs below only ever grow at their end.  A binding compiled
+ * against this header checks kd_fa_abi_version() == KD_FA_ABI_VERSION once,
+ * before its first call (a library with another value lays the structs out
+ * differently).
  */
 #ifndef KD_FA_H
 #define KD_FA_H
@@ -73,8 +85,8 @@ enum {
     KD_FA_ERR_ROPE       = -6,   /* invalid RoPE or norm descriptor       */
     KD_FA_ERR_LAUNCH     = -7,   /* HIP launch failed                     */
     KD_FA_ERR_DEVICE     = -8,   /* no gfx950 device / runtime error      */
-    KD_FA_ERR_SCRATCH    = -9    /* K exceeds the static scratch of
-                                    kd_fa_dit_run_static                  */
+    KD_FA_ERR_SCRATCH    = -9    /* F32 K or V exceeds the static scratch
+                                    of kd_fa_dit_run_static               */
 };
 
 /* A ggml tensor view: struct ggml_tensor's type, ne, nb and data. */
@@ -106,7 +118,19 @@ typedef struct kd_fa_desc {
     float   max_bias;
     float   logit_softcap;
     int32_t prec;
+    /* The type an F32 K and V are cast to (the workspace forms of
+     * kd_fa_rope_run_ws and kd_fa_dit_run only): KD_FA_TYPE_F16 -- or 0,
+     * a zero-initialised field -- as ggml_cast(k, GGML_TYPE_F16) and
+     * ggml_cast(v_perm, GGML_TYPE_F16) in ops::attention
+     * (src/core/ops.hpp:167-169), or KD_FA_TYPE_BF16.  When only one of K
+     * and V is F32 it is cast to the other's type instead.  Ignored when K
+     * and V are both 16-bit.                                              */
+    int32_t cast_type;
 } kd_fa_desc;
+
+/* Layout version of the structs in this header. */
+#define KD_FA_ABI_VERSION 3
+int kd_fa_abi_version(void);
 
 /* RoPE operand rotation modes for kd_fa_rope_run. */
 enum {
@@ -197,12 +221,17 @@ int kd_fa_rope_run(const kd_fa_desc *desc, const kd_fa_rope *rope, void *stream)
  * rotated K afterwards.  workspace_bytes must be at least
  * kd_fa_rope_workspace_size(desc) and workspace 16-byte aligned
  * (KD_FA_ERR_LAYOUT otherwise, KD_FA_ERR_NULL when it is NULL).  The library
- * still allocates nothing.
+ * still allocates nothing.  K and V may also be F32 here (the rotation's
+ * F32 output and the V projection that ops::attention casts,
+ * src/core/ops.hpp:167-169): the same pass casts them, K after its
+ * rotation, to desc->cast_type, V into the workspace after K (at a 256-byte
+ * boundary); the result is kd_fa_rope_run's on the cast operands.
  */
 int kd_fa_rope_run_ws(const kd_fa_desc *desc, const kd_fa_rope *rope, void *workspace,
                       size_t workspace_bytes, void *stream);
 
-/* Bytes of K-sized workspace kd_fa_rope_run_ws needs (0 for an invalid node). */
+/* Bytes of workspace kd_fa_rope_run_ws needs: the rotated K, plus the cast
+ * V when V is F32 (0 for an invalid node). */
 size_t kd_fa_rope_workspace_size(const kd_fa_desc *desc);
 
 /*
@@ -231,16 +260,18 @@ typedef struct kd_fa_qk_norm {
  * every step in F32 as kd_fa_qk_norm and kd_fa_rope_run state.
  * workspace != NULL: K is transformed once into it (as kd_fa_rope_run_ws,
  * same size rule; it holds k' afterwards); NULL: K tiles are transformed
- * on load.  The two give bitwise equal results.  K may be F32 -- the
- * projection output, normalised and rotated before the one rounding to V's
- * type, the reference's order (ops.hpp:167 casts after RoPE) -- when K is
- * transformed (a K norm weight or a RoPE mode); the workspace is then
- * mandatory (KD_FA_ERR_NULL without one).  kd_fa_dit_supports accepts an
- * F32 K on exactly that condition.  With kd_fa_workspace_size(desc, rope,
- * norm) bytes, a masked short-key node (the cross-attention) also keeps its
- * mask summary there, after K (as kd_fa_run_ws).
- * norm == NULL and rope == NULL is kd_fa_run (kd_fa_run_ws with a
- * workspace).
+ * on load.  The two give bitwise equal results.  K and V may be F32 -- the
+ * projection outputs as ops::attention receives them: K normalised and
+ * rotated before its one rounding, the reference's order (ops.hpp:167
+ * casts after RoPE), V cast as stored (ops.hpp:168-169), both to
+ * desc->cast_type by the one pre-pass launch that writes the transformed K
+ * (V after K in the workspace).  The workspace is then mandatory
+ * (KD_FA_ERR_NULL without one); kd_fa_dit_supports answers for this
+ * workspace form, so it accepts F32 K and V.  With
+ * kd_fa_workspace_size(desc, rope, norm) bytes, a masked short-key node
+ * (the cross-attention) also keeps its mask summary there, after K and V
+ * (as kd_fa_run_ws).  norm == NULL and rope == NULL with 16-bit K and V is
+ * kd_fa_run (kd_fa_run_ws with a workspace).
  */
 int kd_fa_dit_run(const kd_fa_desc *desc, const kd_fa_rope *rope, const kd_fa_qk_norm *norm,
                   void *workspace, size_t workspace_bytes, void *stream);
@@ -248,11 +279,12 @@ int kd_fa_dit_run(const kd_fa_desc *desc, const kd_fa_rope *rope, const kd_fa_qk
 /*
  * Bytes of workspace kd_fa_run_ws, kd_fa_rope_run_ws and kd_fa_dit_run can
  * use for the node (0 for an invalid node or one that uses none): the
- * transformed K (kd_fa_rope_workspace_size bytes) when rope or a key norm
- * transforms K, then, 256-byte aligned, the mask summary of a masked
- * short-key node (4 bytes per mask batch, mask head and 32 query rows); for
- * a D = 512 node with a key split, its partial results (2,056 bytes per
- * query row and key range).
+ * transformed K when rope or a key norm transforms K or K is F32, then,
+ * 256-byte aligned, the cast V when V is F32 (together
+ * kd_fa_rope_workspace_size bytes), then, 256-byte aligned, the mask
+ * summary of a masked short-key node (4 bytes per mask batch, mask head and
+ * 32 query rows); for a D = 512 node with a key split, its partial results
+ * (2,056 bytes per query row and key range).
  */
 size_t kd_fa_workspace_size(const kd_fa_desc *desc, const kd_fa_rope *rope, const kd_fa_qk_norm *norm);
 
@@ -304,14 +336,19 @@ int kd_fa_rope_text_table(int L, int D, float theta, float *out);
  * device memory (code under stream capture, tight serving loops, harnesses
  * that forbid hipMalloc).  The caller passes inputs and outputs only; the
  * library allocates nothing, and the array (KD_FA_STATIC_SCRATCH_BYTES per
- * GPU, held until the process ends) is set up on the first call on each
- * device.  A node whose transformed K (the kd_fa_rope_workspace_size bytes)
- * exceeds the array is refused with KD_FA_ERR_SCRATCH before any device
- * work; a node that transforms no K needs no K workspace and always runs.
- * The array also holds what kd_fa_workspace_size counts beyond K (the mask
- * summary, the D = 512 key split's partial results) when that fits; else
- * the call runs without it.  The result is bitwise equal to kd_fa_dit_run's
- * with a caller workspace of the same size.
+ * GPU, held until the process ends) is looked up (hipGetSymbolAddress) on
+ * the first call on each device; make that first call outside stream
+ * capture (a lookup that fails is retried on the next call).  A node whose
+ * transformed K and cast V (the kd_fa_rope_workspace_size bytes) exceed the
+ * array runs as kd_fa_dit_run without a workspace when K and V are 16-bit
+ * (K then transformed in staged groups or on load: the same result,
+ * bitwise), and is refused with KD_FA_ERR_SCRATCH before any device work
+ * when K or V is F32 (their cast needs the workspace); a node that
+ * transforms no K needs no K workspace and always runs.  The array also
+ * holds what kd_fa_workspace_size counts beyond K and V (the mask summary,
+ * the D = 512 key split's partial results) when that fits; else the call
+ * runs without it.  The result is bitwise equal to kd_fa_dit_run's with a
+ * caller workspace of the same size.
  * Every call on a GPU shares that GPU's array: calls that overlap on one
  * GPU (two streams, two host threads) race and must be serialised by the
  * caller.

@@ -26,22 +26,36 @@ size_t elem_size(int type) { return type == KD_FA_TYPE_F32 ? 4 : 2; }
 bool is_16b(uint64_t x) { return (x & 15u) == 0; }
 bool is_16b(const void *p) { return is_16b(reinterpret_cast<uintptr_t>(p)); }
 
+bool is_16bit(int type) { return type == KD_FA_TYPE_F16 || type == KD_FA_TYPE_BF16; }
+
+// The MFMA operand type of the call: K's and V's when they are 16-bit; an
+// F32 K or V (the workspace forms) is cast to the other's 16-bit type, or,
+// when both are F32, to desc->cast_type (F16 unless BF16 is asked for: the
+// ggml_cast of ops.hpp:167-169).
+int op_type(const kd_fa_desc *d) {
+    if (is_16bit(d->v.type)) return d->v.type;
+    if (is_16bit(d->k.type)) return d->k.type;
+    return d->cast_type == KD_FA_TYPE_BF16 ? KD_FA_TYPE_BF16 : KD_FA_TYPE_F16;
+}
+
 // Conditions of kd_fa_supports (and of the RoPE and norm descriptors when
 // given).  `mask_vec` reports whether the mask rows can be read 16 bytes at
 // a time.
-// k_f32: an F32 K is accepted (K is transformed, by a norm weight or RoPE;
-// run() then also requires the workspace, whose pre-pass rounds K to V's
-// type).
+// kv_f32: an F32 K and V are accepted (the workspace forms, whose pre-pass
+// casts them; run() then also requires the workspace).
 int validate(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, bool *mask_vec,
-             bool k_f32 = false) {
+             bool kv_f32 = false) {
     if (!d) return KD_FA_ERR_NULL;
     const kd_fa_tensor &q = d->q, &k = d->k, &v = d->v, &m = d->mask, &o = d->dst;
     if (!q.data || !k.data || !v.data || !o.data) return KD_FA_ERR_NULL;
 
     // types: Q is converted to K's type on load; K and V share one MFMA type
+    // (an F32 K or V is cast to it by the workspace pre-pass)
     if (q.type != KD_FA_TYPE_F32 && q.type != KD_FA_TYPE_F16 && q.type != KD_FA_TYPE_BF16) return KD_FA_ERR_TYPE;
-    if (v.type != KD_FA_TYPE_F16 && v.type != KD_FA_TYPE_BF16) return KD_FA_ERR_TYPE;
-    if (k.type != v.type && !(k_f32 && k.type == KD_FA_TYPE_F32)) return KD_FA_ERR_TYPE;
+    const bool k32 = kv_f32 && k.type == KD_FA_TYPE_F32, v32 = kv_f32 && v.type == KD_FA_TYPE_F32;
+    if ((!is_16bit(k.type) && !k32) || (!is_16bit(v.type) && !v32)) return KD_FA_ERR_TYPE;
+    if (k.type != v.type && !k32 && !v32) return KD_FA_ERR_TYPE;
+    if ((k32 || v32) && d->cast_type != 0 && !is_16bit(d->cast_type)) return KD_FA_ERR_TYPE;
     // dst: the node's F32, or a 16-bit cast of it
     if (o.type != KD_FA_TYPE_F32 && o.type != KD_FA_TYPE_F16 && o.type != KD_FA_TYPE_BF16) return KD_FA_ERR_TYPE;
     if (m.data && m.type != KD_FA_TYPE_F16) return KD_FA_ERR_TYPE;
@@ -91,6 +105,7 @@ int validate(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, b
     // D = 512 (the VAE attention block): the plain node only -- no mask, no
     // RoPE, no RMSNorm; 32-row query tiles; 32-bit V row offsets
     if (D == kHeadDimVae) {
+        if (k32 || v32) return KD_FA_ERR_TYPE;
         if (m.data) return KD_FA_ERR_SHAPE;
         if ((r && r->mode != KD_FA_ROPE_NONE) || (n && (n->q_weight || n->k_weight))) return KD_FA_ERR_ROPE;
         if (H > 0 && B > 0 && (Lq + 31) / 32 > kI32Max / H / B) return KD_FA_ERR_SHAPE;
@@ -151,11 +166,7 @@ int device_ok() {
     return st == 1 ? KD_FA_OK : KD_FA_ERR_DEVICE;
 }
 
-// K-sized workspace in the attention's operand type (V's)
-size_t rope_ws_bytes(const kd_fa_desc *d) {
-    return (size_t)kHeadDim * (size_t)d->k.ne[1] * (size_t)d->k.ne[2] * (size_t)d->k.ne[3] *
-           elem_size(d->v.type);
-}
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
 // Key split of the D = 512 kernel through the workspace (kd_fa_run_ws):
 // when its 32-row workgroups would leave CUs idle (fewer than 256: the VAE's
@@ -186,13 +197,6 @@ D512Split d512_split(int64_t Lq, int64_t Lk, int64_t H, int64_t B, int route) {
     return r;
 }
 
-// The workspace holds the transformed K (when K is transformed) and, after
-// it at a 256-byte boundary, the mask summary of a masked call whose key set
-// the short-key kernel can hold (one 32-bit word per mask batch, mask head
-// and 32-row query block).
-size_t summary_offset(const kd_fa_desc *d, bool k_xform) {
-    return k_xform ? (rope_ws_bytes(d) + 255) / 256 * 256 : 0;
-}
 // The summary pass costs a launch and one read of the mask (~9 us at the
 // 31,744-token cross-attention, whose kernel it shortens by ~33 us); below
 // 65,536 query rows in all (2,048 tokens x 32 heads) the launch is not paid
@@ -200,9 +204,35 @@ size_t summary_offset(const kd_fa_desc *d, bool k_xform) {
 // masked short-key node that has the workspace (for comparisons).
 bool summary_pays(int64_t rows, int route) { return (route & KD_FA_ROUTE_SUMMARY) || rows >= 65536; }
 
-size_t summary_bytes(const kd_fa_desc *d, bool rope_on) {
-    if (!d->mask.data || rope_on || d->q.ne[0] != kHeadDim || d->k.ne[1] > kdfa::kXresMaxKeys) return 0;
-    return 4 * (size_t)d->mask.ne[3] * (size_t)d->mask.ne[2] * (size_t)((d->q.ne[1] + 31) / 32);
+// The workspace of a D = 128 node, each part at a 256-byte boundary: the
+// transformed K (when K is normalised, rotated or F32: contiguous
+// [D, Lk, Hk, Bk] in the operand type), the cast V (when V is F32:
+// contiguous [D, Lk, Hv, Bv]), then the mask summary of a masked call whose
+// key set the short-key kernel can hold (one 32-bit word per mask batch,
+// mask head and 32-row query block).  `cast` is the end of the K and V
+// parts (kd_fa_rope_workspace_size).
+struct WsLayout {
+    bool k_ws = false, v_ws = false;
+    size_t k_bytes = 0, v_off = 0, v_bytes = 0, cast = 0, s_off = 0, s_bytes = 0, total = 0;
+};
+// (force_k: K has a part whatever the descriptors say -- the rotated K of
+// kd_fa_rope_run_ws, sized before its RoPE descriptor is known.)
+WsLayout ws_layout(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, bool force_k = false) {
+    WsLayout w;
+    const bool rope_on = r && r->mode != KD_FA_ROPE_NONE;
+    w.k_ws = force_k || rope_on || (n && n->k_weight) || d->k.type == KD_FA_TYPE_F32;
+    w.v_ws = d->v.type == KD_FA_TYPE_F32;
+    const size_t row = (size_t)kHeadDim * 2, lk = (size_t)d->k.ne[1];
+    if (w.k_ws) w.k_bytes = row * lk * (size_t)d->k.ne[2] * (size_t)d->k.ne[3];
+    w.v_off = w.k_ws ? align256(w.k_bytes) : 0;
+    if (w.v_ws) w.v_bytes = row * lk * (size_t)d->v.ne[2] * (size_t)d->v.ne[3];
+    w.cast = w.v_ws ? w.v_off + w.v_bytes : w.k_bytes;
+    if (d->mask.data && !rope_on && d->k.ne[1] <= kdfa::kXresMaxKeys) {
+        w.s_off = w.cast ? align256(w.cast) : 0;
+        w.s_bytes = 4 * (size_t)d->mask.ne[3] * (size_t)d->mask.ne[2] * (size_t)((d->q.ne[1] + 31) / 32);
+    }
+    w.total = w.s_bytes ? w.s_off + w.s_bytes : w.cast;
+    return w;
 }
 
 // K is transformed (normalised and / or rotated) when a norm weight or a
@@ -240,10 +270,10 @@ static bool use_w64(const kdfa::Args &a, bool k_on_load, int route) {
 // or in K's type, and a mask's rows are 16-byte aligned and hold every
 // 8-key chunk that starts below Lk.  KD_FA_ROUTE_NO_XRES routes them to the
 // 32-row kernel (for comparisons).
-static bool use_xres(const kdfa::Args &a, const kd_fa_desc *d, bool k_on_load, int route) {
+static bool use_xres(const kdfa::Args &a, int op, const kd_fa_desc *d, bool k_on_load, int route) {
     if ((route & KD_FA_ROUTE_NO_XRES) || k_on_load || a.rope_mode != KD_FA_ROPE_NONE) return false;
     if (a.Lk > kdfa::kXresMaxKeys) return false;
-    if (a.q_type != KD_FA_TYPE_F32 && a.q_type != d->v.type) return false;
+    if (a.q_type != KD_FA_TYPE_F32 && a.q_type != op) return false;
     if (a.m && (!a.mask_vec || d->mask.ne[0] < ((int64_t)a.Lk + 7) / 8 * 8)) return false;
     return true;
 }
@@ -277,8 +307,54 @@ static void xres_split(kdfa::Args &a) {
 // (one or two heads), which has no later rows to borrow and rotates K on
 // load.  The transformed values are the pre-pass's, so the result is
 // bitwise that of the workspace path.  Groups stay within one batch.
-bool staged_ok(const kdfa::Args &a, const kd_fa_desc *d, int route) {
+// Byte range [lo, hi) a tensor view spans (empty for a NULL or empty view).
+struct Range {
+    uintptr_t lo = 0, hi = 0;
+};
+Range view_range(const kd_fa_tensor &t) {
+    Range r;
+    if (!t.data) return r;
+    uint64_t span = elem_size(t.type);
+    for (int i = 0; i < 4; ++i) {
+        if (t.ne[i] <= 0) return r;
+        span += (uint64_t)(t.ne[i] - 1) * t.nb[i];
+    }
+    r.lo = reinterpret_cast<uintptr_t>(t.data);
+    r.hi = r.lo + span;
+    return r;
+}
+Range ptr_range(const void *p, size_t bytes) {
+    Range r;
+    if (p) {
+        r.lo = reinterpret_cast<uintptr_t>(p);
+        r.hi = r.lo + bytes;
+    }
+    return r;
+}
+bool overlaps(const Range &a, const Range &b) { return a.lo < b.hi && b.lo < a.hi; }
+
+// Whether dst shares bytes with an operand of the call.  The header requires
+// that it does not; the staged path, which writes transformed K into output
+// rows ahead of the attention, is only taken when this is checked false.
+bool dst_overlaps_operands(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n) {
+    const Range o = view_range(d->dst);
+    if (overlaps(o, view_range(d->q)) || overlaps(o, view_range(d->k)) || overlaps(o, view_range(d->v)) ||
+        overlaps(o, view_range(d->mask)))
+        return true;
+    if (r && r->mode == KD_FA_ROPE_TABLE && overlaps(o, view_range(r->table))) return true;
+    if (r && r->mode == KD_FA_ROPE_AXES) {
+        const size_t floats = (size_t)r->grid[0] * r->axes[0] + (size_t)r->grid[1] * r->axes[1] +
+                              (size_t)r->grid[2] * r->axes[2];
+        if (overlaps(o, ptr_range(r->axes_data, floats * 4))) return true;
+    }
+    if (n && (overlaps(o, ptr_range(n->q_weight, kHeadDim * 4)) || overlaps(o, ptr_range(n->k_weight, kHeadDim * 4))))
+        return true;
+    return false;
+}
+
+bool staged_ok(const kdfa::Args &a, const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, int route) {
     if ((route & KD_FA_ROUTE_NO_W64) || a.m) return false;
+    if (dst_overlaps_operands(d, r, n)) return false;
     if (a.rk2 != 1 || a.rk3 != 1 || a.rv2 != 1 || a.rv3 != 1) return false;
     if (a.Lk < 64 || a.Lq < a.Lk || !w64_tail_ok(a)) return false;
     const int64_t row = kHeadDim * (int64_t)elem_size(d->dst.type);
@@ -308,11 +384,15 @@ kdfa::Args head_range(const kdfa::Args &a, int b, int h0, int n) {
 // times) under the constraints: each group at most `ratio` times the heads
 // of the next (whose output rows hold its transformed K) and within one
 // batch; the last group has 1 to 8 heads.  A dynamic program over (pairs
-// left, size of the next group), O(P^3) per last-group size for P (b, h)
-// pairs, remembered for the last shape of the calling thread.  The cost is
-// in the same units as onload_cost's, the one launch that rotates K on load
+// left, size of the next group): a group never spans batches, so the next
+// group's size is at most H, and the program takes O(P H^2) steps and
+// O(P H) memory per last-group size for P (b, h) pairs.  Calls with more
+// than kStagedMaxPairs pairs are not staged (an empty plan: K on load).
+// The last few plans of the calling thread are remembered.  The cost is in
+// the same units as onload_cost's, the one launch that rotates K on load
 // for every pair.
 constexpr double kStagedLaunch = 0.05, kStagedOnLoad = 1.4;
+constexpr int kStagedMaxPairs = 4096;
 double launch_rounds(int heads, int wg_head) { return (double)(((int64_t)heads * wg_head + 255) / 256); }
 double onload_cost(int P, int wg_head) { return kStagedOnLoad * launch_rounds(P, wg_head); }
 struct StagedPlan {
@@ -324,48 +404,54 @@ StagedPlan staged_groups(int P, int H, int wg_head, int ratio) {
         int P = -1, H = -1, wg = -1, ratio = -1;
         StagedPlan plan;
     };
-    thread_local Memo memo;
-    if (memo.P == P && memo.H == H && memo.wg == wg_head && memo.ratio == ratio) return memo.plan;
-    auto rounds = [wg_head](int h) { return launch_rounds(h, wg_head); };
-    constexpr double kLaunch = kStagedLaunch, kOnLoad = kStagedOnLoad;
-    double best_cost = 1e300;
-    std::vector<int> best;
-    std::vector<double> dp((size_t)(P + 1) * (P + 1));
-    std::vector<int> pick((size_t)(P + 1) * (P + 1));
-    for (int n_last = 1; n_last <= 8; ++n_last) {
-        if (n_last > H || n_last >= P) continue;
-        const int E = P - n_last;
-        for (int s = 1; s <= P; ++s) dp[s] = 0.0;   // e = 0
-        for (int e = 1; e <= E; ++e) {
-            const int avail = e - ((e - 1) / H) * H;   // pairs of its batch before e
-            for (int s = 1; s <= P; ++s) {
-                double b = 1e300;
-                int bh = 0;
-                const int top = std::min(ratio * s, avail);
-                for (int h = 1; h <= top; ++h) {
-                    const double c = rounds(h) + kLaunch + dp[(size_t)(e - h) * (P + 1) + h];
-                    if (c < b - 1e-12 || (c < b + 1e-12 && h > bh)) { b = c; bh = h; }
+    constexpr int kMemo = 4;
+    thread_local Memo memo[kMemo];
+    thread_local int memo_next = 0;
+    for (const Memo &m : memo)
+        if (m.P == P && m.H == H && m.wg == wg_head && m.ratio == ratio) return m.plan;
+    StagedPlan plan;
+    if (P <= kStagedMaxPairs && H >= 1) {
+        auto rounds = [wg_head](int h) { return launch_rounds(h, wg_head); };
+        constexpr double kLaunch = kStagedLaunch, kOnLoad = kStagedOnLoad;
+        const size_t W = (size_t)H + 1;   // next-group sizes 1..H
+        std::vector<double> dp((size_t)(P + 1) * W);
+        std::vector<int> pick((size_t)(P + 1) * W);
+        for (int n_last = 1; n_last <= 8; ++n_last) {
+            if (n_last > H || n_last >= P) continue;
+            const int E = P - n_last;
+            for (int s = 1; s <= H; ++s) dp[s] = 0.0;   // e = 0
+            for (int e = 1; e <= E; ++e) {
+                const int avail = e - ((e - 1) / H) * H;   // pairs of its batch before e
+                for (int s = 1; s <= H; ++s) {
+                    double b = 1e300;
+                    int bh = 0;
+                    const int top = std::min(ratio * s, avail);
+                    for (int h = 1; h <= top; ++h) {
+                        const double c = rounds(h) + kLaunch + dp[(size_t)(e - h) * W + h];
+                        if (c < b - 1e-12 || (c < b + 1e-12 && h > bh)) { b = c; bh = h; }
+                    }
+                    dp[(size_t)e * W + s] = b;
+                    pick[(size_t)e * W + s] = bh;
                 }
-                dp[(size_t)e * (P + 1) + s] = b;
-                pick[(size_t)e * (P + 1) + s] = bh;
             }
-        }
-        const double cost = dp[(size_t)E * (P + 1) + n_last] + kOnLoad * rounds(n_last);
-        if (cost < best_cost) {
-            best_cost = cost;
-            best.clear();
-            for (int e = E, s = n_last; e > 0;) {
-                const int h = pick[(size_t)e * (P + 1) + s];
-                best.push_back(h);
-                e -= h;
-                s = h;
+            const double cost = dp[(size_t)E * W + n_last] + kOnLoad * rounds(n_last);
+            if (cost < plan.cost) {
+                plan.cost = cost;
+                plan.sizes.clear();
+                for (int e = E, s = n_last; e > 0;) {
+                    const int h = pick[(size_t)e * W + s];
+                    plan.sizes.push_back(h);
+                    e -= h;
+                    s = h;
+                }
+                std::reverse(plan.sizes.begin(), plan.sizes.end());
+                plan.sizes.push_back(n_last);
             }
-            std::reverse(best.begin(), best.end());
-            best.push_back(n_last);
         }
     }
-    memo = {P, H, wg_head, ratio, {best, best_cost}};
-    return memo.plan;
+    memo[memo_next] = {P, H, wg_head, ratio, plan};
+    memo_next = (memo_next + 1) % kMemo;
+    return plan;
 }
 
 // The staged plan of a call that staged_ok allows.
@@ -415,17 +501,20 @@ int run_staged(const kdfa::Args &a, const std::vector<int> &sizes, int kv_type, 
     return kdfa::launch(s, kv_type, true, waves, hs) == hipSuccess ? KD_FA_OK : KD_FA_ERR_LAUNCH;
 }
 
+// kv_f32: the entry point accepts an F32 K and V (the workspace forms).
 int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *ws, size_t ws_bytes,
-        void *stream) {
+        void *stream, bool kv_f32) {
     bool mask_vec = false;
-    const bool rope_on = r && r->mode != KD_FA_ROPE_NONE;
-    const bool k_xform = rope_on || (n && n->k_weight);
-    int st = validate(d, r, n, &mask_vec, k_xform);
+    int st = validate(d, r, n, &mask_vec, kv_f32);
     if (st != KD_FA_OK) return st;
-    // an F32 K is rounded to V's type by the workspace pre-pass only
-    if (!ws && k_xform && d->k.type == KD_FA_TYPE_F32) return KD_FA_ERR_NULL;
+    const bool v32 = d->v.type == KD_FA_TYPE_F32;
+    const WsLayout wl = ws_layout(d, r, n);
+    const bool k_xform = wl.k_ws;   // normalised, rotated or cast from F32
+    // an F32 K or V is cast to the operand type by the workspace pre-pass only
+    if (!ws && (d->k.type == KD_FA_TYPE_F32 || v32)) return KD_FA_ERR_NULL;
     if (ws && !is_16b(ws)) return KD_FA_ERR_LAYOUT;
-    if (ws && k_xform && ws_bytes < rope_ws_bytes(d)) return KD_FA_ERR_LAYOUT;
+    if (ws && wl.cast && ws_bytes < wl.cast) return KD_FA_ERR_LAYOUT;
+    const int T = op_type(d);   // the MFMA operand type
     const int route = g_route.load(std::memory_order_relaxed);
     const int64_t Lq = d->q.ne[1], H = d->q.ne[2], B = d->q.ne[3];
     if (Lq == 0 || H == 0 || B == 0) return KD_FA_OK;
@@ -489,54 +578,76 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
             a.part = static_cast<float *>(ws);
             a.n_split = sp.S;
             a.split_keys = sp.keys;
-            if (kdfa::launch_d512(a, d->v.type, rows, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
+            if (kdfa::launch_d512(a, T, rows, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
             return kdfa::launch_d512_combine(a, hs) == hipSuccess ? KD_FA_OK : KD_FA_ERR_LAUNCH;
         }
-        return kdfa::launch_d512(a, d->v.type, rows, hs) == hipSuccess ? KD_FA_OK : KD_FA_ERR_LAUNCH;
+        return kdfa::launch_d512(a, T, rows, hs) == hipSuccess ? KD_FA_OK : KD_FA_ERR_LAUNCH;
     }
     bool k_rope = k_xform && !ws;
-    if (k_rope && staged_ok(a, d, route)) {
+    if (k_rope && staged_ok(a, d, r, n, route)) {
         const StagedPlan plan = staged_plan(a);
-        if (staged_pays(a, plan, route)) return run_staged(a, plan.sizes, d->v.type, hs);
+        if (staged_pays(a, plan, route)) return run_staged(a, plan.sizes, T, hs);
     }
     // a mask row block shared by every head is read once per q-tile when the
     // heads of a q-tile run back to back (K and V of all heads then share the
     // L2 instead, which the short text keys of the cross-attention allow)
     a.heads_inner = (a.m && d->mask.ne[2] == 1 && H > 1 && d->k.ne[1] <= 1024) ? 1 : 0;
 
-    if (ws && k_xform) {
+    if (ws && (k_xform || v32)) {
+        // the pre-pass: K normalised / rotated / cast and an F32 V cast, in
+        // one launch when K and V have the same heads and batches
+        char *const wsc = static_cast<char *>(ws);
         const int hk = (int)d->k.ne[2], bk = (int)d->k.ne[3];
-        const int64_t row = kHeadDim * (int64_t)elem_size(d->v.type);
-        const kdfa::KStrides st = {row, row * a.Lk, row * a.Lk * hk};
-        if (kdfa::launch_rope_k(a, d->v.type, hk, bk, ws, st, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
-        a.k = static_cast<const char *>(ws);
-        a.k_nb1 = row;
-        a.k_nb2 = row * a.Lk;
-        a.k_nb3 = row * a.Lk * hk;
+        const int hv = (int)d->v.ne[2], bv = (int)d->v.ne[3];
+        const int64_t row = kHeadDim * 2;
+        const kdfa::KStrides kst = {row, row * a.Lk, row * a.Lk * hk};
+        const kdfa::KStrides vst = {row, row * a.Lk, row * a.Lk * hv};
+        char *const kout = k_xform ? wsc : nullptr;
+        char *const vout = v32 ? wsc + wl.v_off : nullptr;
+        hipError_t e = hipSuccess;
+        if (kout && vout && (hk != hv || bk != bv)) {
+            e = kdfa::launch_rope_k(a, T, hk, bk, kout, kst, nullptr, vst, hs);
+            if (e == hipSuccess) e = kdfa::launch_rope_k(a, T, hv, bv, nullptr, kst, vout, vst, hs);
+        } else {
+            e = kout ? kdfa::launch_rope_k(a, T, hk, bk, kout, kst, vout, vst, hs)
+                     : kdfa::launch_rope_k(a, T, hv, bv, nullptr, kst, vout, vst, hs);
+        }
+        if (e != hipSuccess) return KD_FA_ERR_LAUNCH;
+        if (kout) {
+            a.k = kout;
+            a.k_nb1 = row;
+            a.k_nb2 = row * a.Lk;
+            a.k_nb3 = row * a.Lk * hk;
+        }
+        if (vout) {
+            a.v = vout;
+            a.v_nb1 = row;
+            a.v_nb2 = row * a.Lk;
+            a.v_nb3 = row * a.Lk * hv;
+        }
     }
     hipError_t e;
-    if (use_xres(a, d, k_rope, route)) {
+    if (use_xres(a, T, d, k_rope, route)) {
         xres_split(a);
         // with room in the workspace, the mask summary: tiles that are -inf
         // for all rows of a block are then skipped without loading their
         // mask chunks (one L2 round trip per dead tile and block)
-        const size_t s_off = summary_offset(d, k_xform), s_bytes = summary_bytes(d, rope_on);
-        if (a.m && ws && s_bytes && ws_bytes >= s_off + s_bytes && summary_pays(Lq * H * B, route)) {
-            uint32_t *sum = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + s_off);
+        if (a.m && ws && wl.s_bytes && ws_bytes >= wl.s_off + wl.s_bytes && summary_pays(Lq * H * B, route)) {
+            uint32_t *sum = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + wl.s_off);
             if (kdfa::launch_mask_live(a, sum, hs) != hipSuccess) return KD_FA_ERR_LAUNCH;
             a.m_live = sum;
             a.m_live_nqb = (int32_t)((Lq + 31) / 32);
         }
-        e = kdfa::launch_xres(a, d->v.type, hs);
+        e = kdfa::launch_xres(a, T, hs);
     } else if (use_w64(a, k_rope, route)) {
         a.n_qt = (int32_t)((Lq + kdfa::kW64Rows - 1) / kdfa::kW64Rows);
         a.n_blocks = (int32_t)(a.n_qt * H * B);
-        e = kdfa::launch_w64(a, d->v.type, hs);
+        e = kdfa::launch_w64(a, T, hs);
     } else {
         const int waves = kdfa::d128_waves(a.m != nullptr, k_rope, a.Lk);
         a.n_qt = (int32_t)((Lq + 32 * waves - 1) / (32 * waves));
         a.n_blocks = (int32_t)(a.n_qt * H * B);
-        e = kdfa::launch(a, d->v.type, k_rope, waves, hs);
+        e = kdfa::launch(a, T, k_rope, waves, hs);
     }
     if (e != hipSuccess) return KD_FA_ERR_LAUNCH;
     return KD_FA_OK;
@@ -561,25 +672,23 @@ int device_gfx950() { return device_ok(); }
 
 int run_node(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *ws, size_t ws_bytes,
              void *stream) {
-    return run(d, r, n, ws, ws_bytes, stream);
+    return run(d, r, n, ws, ws_bytes, stream, true);
 }
 
-size_t k_workspace_need(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, int *status) {
-    const bool k_xform = (r && r->mode != KD_FA_ROPE_NONE) || (n && n->k_weight);
-    *status = validate(d, r, n, nullptr, k_xform);
-    if (*status != KD_FA_OK || !k_xform || d->q.ne[0] != kHeadDim) return 0;
-    return rope_ws_bytes(d);
+size_t cast_workspace_need(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, int *status,
+                           bool *f32_kv) {
+    *status = validate(d, r, n, nullptr, true);
+    *f32_kv = false;
+    if (*status != KD_FA_OK || d->q.ne[0] != kHeadDim) return 0;
+    *f32_kv = d->k.type == KD_FA_TYPE_F32 || d->v.type == KD_FA_TYPE_F32;
+    return ws_layout(d, r, n).cast;
 }
 
 size_t workspace_need(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, int *status) {
-    const bool rope_on = r && r->mode != KD_FA_ROPE_NONE;
-    const bool k_xform = rope_on || (n && n->k_weight);
-    *status = validate(d, r, n, nullptr, k_xform);
+    *status = validate(d, r, n, nullptr, true);
     if (*status != KD_FA_OK) return 0;
     if (d->q.ne[0] == kHeadDimVae) return d512_split(d->q.ne[1], d->k.ne[1], d->q.ne[2], d->q.ne[3], 0).bytes;
-    const size_t k_need = k_xform && d->q.ne[0] == kHeadDim ? rope_ws_bytes(d) : 0;
-    const size_t s_need = summary_bytes(d, rope_on);
-    return s_need ? summary_offset(d, k_need != 0) + s_need : k_need;
+    return ws_layout(d, r, n).total;
 }
 }  // namespace kdfa
 
@@ -597,10 +706,12 @@ int kd_fa_rope_supports(const kd_fa_desc *desc, const kd_fa_rope *rope, int *rea
     return st == KD_FA_OK ? 1 : 0;
 }
 
-int kd_fa_run(const kd_fa_desc *desc, void *stream) { return run(desc, nullptr, nullptr, nullptr, 0, stream); }
+int kd_fa_run(const kd_fa_desc *desc, void *stream) {
+    return run(desc, nullptr, nullptr, nullptr, 0, stream, false);
+}
 
 int kd_fa_run_ws(const kd_fa_desc *desc, void *workspace, size_t workspace_bytes, void *stream) {
-    return run(desc, nullptr, nullptr, workspace, workspace_bytes, stream);
+    return run(desc, nullptr, nullptr, workspace, workspace_bytes, stream, false);
 }
 
 size_t kd_fa_workspace_size(const kd_fa_desc *desc, const kd_fa_rope *rope, const kd_fa_qk_norm *norm) {
@@ -611,33 +722,32 @@ size_t kd_fa_workspace_size(const kd_fa_desc *desc, const kd_fa_rope *rope, cons
 }
 
 int kd_fa_rope_run(const kd_fa_desc *desc, const kd_fa_rope *rope, void *stream) {
-    return run(desc, rope, nullptr, nullptr, 0, stream);
+    return run(desc, rope, nullptr, nullptr, 0, stream, false);
 }
 
 int kd_fa_dit_supports(const kd_fa_desc *desc, const kd_fa_rope *rope, const kd_fa_qk_norm *norm,
                        int *reason) {
-    // an F32 K only when K is transformed (then through the workspace)
-    const bool k_xform = (rope && rope->mode != KD_FA_ROPE_NONE) || (norm && norm->k_weight);
-    const int st = validate(desc, rope, norm, nullptr, k_xform);
+    // the workspace form: an F32 K and V are cast by its pre-pass
+    const int st = validate(desc, rope, norm, nullptr, true);
     if (reason) *reason = st;
     return st == KD_FA_OK ? 1 : 0;
 }
 
 int kd_fa_dit_run(const kd_fa_desc *desc, const kd_fa_rope *rope, const kd_fa_qk_norm *norm,
                   void *workspace, size_t workspace_bytes, void *stream) {
-    return run(desc, rope, norm, workspace, workspace_bytes, stream);
+    return run(desc, rope, norm, workspace, workspace_bytes, stream, true);
 }
 
 size_t kd_fa_rope_workspace_size(const kd_fa_desc *desc) {
-    if (!desc || validate(desc, nullptr, nullptr, nullptr, true) != KD_FA_OK) return 0;
-    return rope_ws_bytes(desc);
+    if (!desc || validate(desc, nullptr, nullptr, nullptr, true) != KD_FA_OK || desc->q.ne[0] != kHeadDim) return 0;
+    return ws_layout(desc, nullptr, nullptr, true).cast;
 }
 
 int kd_fa_rope_run_ws(const kd_fa_desc *desc, const kd_fa_rope *rope, void *workspace,
                       size_t workspace_bytes, void *stream) {
     if (!workspace && rope && rope->mode != KD_FA_ROPE_NONE && desc && desc->k.ne[1] > 0)
         return KD_FA_ERR_NULL;
-    return run(desc, rope, nullptr, workspace, workspace_bytes, stream);
+    return run(desc, rope, nullptr, workspace, workspace_bytes, stream, true);
 }
 
 // rope::compute_visual_rope (src/rope.hpp:56-102).
@@ -725,7 +835,9 @@ const char *kd_fa_strerror(int status) {
     }
 }
 
-int kd_fa_version(void) { return 200; }
+int kd_fa_version(void) { return 300; }
+
+int kd_fa_abi_version(void) { return KD_FA_ABI_VERSION; }
 
 int kd_fa_set_routing(int flags) { return g_route.exchange(flags); }
 

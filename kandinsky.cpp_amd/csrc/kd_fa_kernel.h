@@ -27,7 +27,7 @@ struct Args {
     int32_t rv2, rv3;   // H / Hv, B / Bv
     int32_t m_ne2, m_ne3;
     int32_t q_type;     // KD_FA_TYPE_*
-    int32_t k_type;     // K as stored (F32 only for the K pre-pass)
+    int32_t k_type;     // K as stored (F32 only for the K pre-pass; V is F32 when cast)
     int32_t mask_vec;   // mask rows are 16-byte aligned
     float scale_log2;   // scale * log2(e)
     int32_t rope_mode;  // KD_FA_ROPE_*
@@ -69,12 +69,15 @@ int device_gfx950();
 int run_node(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *ws, size_t ws_bytes,
              void *stream);
 
-// Bytes of K-sized workspace the node needs (0 when K is not transformed);
-// *status gets the node's validation status (host-only).
-size_t k_workspace_need(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, int *status);
+// Bytes of workspace the node needs for its transformed K and cast V (0
+// when K is not transformed and V is not F32); *status gets the node's
+// validation status in the workspace form, *f32_kv whether K or V is F32
+// (then the workspace is mandatory).  Host-only.
+size_t cast_workspace_need(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, int *status,
+                           bool *f32_kv);
 
 // Bytes of workspace the node can use (kd_fa_workspace_size): the
-// transformed K, then the mask summary of a masked short-key call.
+// transformed K and cast V, then the mask summary of a masked short-key call.
 size_t workspace_need(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, int *status);
 
 // Enqueue the 32-row kernel for K/V element type kv_type on `stream`, with
@@ -115,10 +118,18 @@ struct KStrides {
     int64_t key, head, batch;
 };
 
-// Normalise (kn_w) and rotate (RoPE mode) K ([D, Lk, H/rk2, B/rk3] through
-// a.k and its strides) into `out` with strides `st`, in K's type.
-hipError_t launch_rope_k(const Args &a, int kv_type, int k_heads, int k_batch, void *out, const KStrides &st,
-                         hipStream_t stream);
+// The pre-pass: normalise (kn_w), rotate (RoPE mode) and round K
+// ([D, Lk, H/rk2, B/rk3] through a.k and its strides, a.k_type) into `out`
+// with strides `st`, and cast an F32 V (through a.v) into `vout` with
+// strides `vst`, both in the operand type kv_type; `heads` x `batch` (b, h)
+// pairs of K (of V when out is nullptr; with both, K and V have the same
+// heads and batches).  Either output may be nullptr.
+hipError_t launch_rope_k(const Args &a, int kv_type, int heads, int batch, void *out, const KStrides &st,
+                         void *vout, const KStrides &vst, hipStream_t stream);
+inline hipError_t launch_rope_k(const Args &a, int kv_type, int heads, int batch, void *out, const KStrides &st,
+                                hipStream_t stream) {
+    return launch_rope_k(a, kv_type, heads, batch, out, st, nullptr, st, stream);
+}
 
 // Waves per workgroup of the 32-row kernel (32 query rows each): 8 (two per
 // SIMD, one workgroup per CU) when it transforms K tiles on load and for
@@ -126,10 +137,7 @@ hipError_t launch_rope_k(const Args &a, int kv_type, int k_heads, int k_batch, v
 // two independent workgroups per CU, each one's Q load and O store
 // overlapping the other's key loop (the masked text cross-attention, and
 // the unmasked one with a long prompt).
-#ifndef KD_FA_SHORT_KEYS
-#define KD_FA_SHORT_KEYS 896   // tuning switch for variant builds
-#endif
-constexpr int kShortKeys = KD_FA_SHORT_KEYS;
+constexpr int kShortKeys = 896;
 constexpr int d128_waves(bool masked, bool k_on_load, int Lk) {
     return k_on_load ? 8 : (masked || Lk <= kShortKeys) ? 4 : 8;
 }

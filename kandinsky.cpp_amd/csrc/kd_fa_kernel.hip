@@ -68,40 +68,13 @@ template <int PRE, int VPM> __device__ __forceinline__ void sched_pipe() {
     sched_pipe_step<6, PRE, VPM>(); sched_pipe_step<7, PRE, VPM>();
 }
 
-// Software-pipelined key loop for the kernels that stream K by DMA (no
-// mask): the S^T product of tile t+1 is interleaved with the softmax of
-// tile t in the same wave (tuning switch; 0 = one phase after the other).
-#ifndef KD_FA_PIPE
-#define KD_FA_PIPE 1
-#endif
-#ifndef KD_FA_PIPE_VPM
-#define KD_FA_PIPE_VPM 6
-#endif
-
-// Wave priority around the MFMA sections (tuning switch).
-#ifndef KD_FA_SETPRIO
-#define KD_FA_SETPRIO 0
-#endif
-// K-fragment prefetch distance (k-steps) and the explicit DS-read / MFMA
-// interleave of S^T = K Q^T (for the kernels that rotate K tiles on load,
-// which hold more registers, separately)
-#ifndef KD_FA_KPRE
-#define KD_FA_KPRE 2
-#endif
-#ifndef KD_FA_SCHED
-#define KD_FA_SCHED 1
-#endif
-#ifndef KD_FA_KPRE_KR
-#define KD_FA_KPRE_KR 0
-#endif
-#ifndef KD_FA_SCHED_KR
-#define KD_FA_SCHED_KR 0
-#endif
-#if KD_FA_SETPRIO
-#define KD_FA_PRIO(x) __builtin_amdgcn_s_setprio(x)
-#else
-#define KD_FA_PRIO(x) ((void)0)
-#endif
+// K-fragment prefetch distance (k-steps ahead of their MFMAs) of the
+// kernels that stream K by DMA, and the VALU instructions placed after each
+// MFMA of the pipelined step (sched_pipe).  The kernel that transforms K
+// tiles on load holds more registers and reads its fragments with no
+// prefetch and no explicit interleave.
+constexpr int kKPreDma = 2;
+constexpr int kPipeVpm = 6;
 
 // Q fragments of query row q_ld (B operands of S^T = K Q^T, k-steps of 16):
 // this lane holds elements ks*16 + hi*8 .. +7 of each k-step; the lane
@@ -441,7 +414,7 @@ void fa_fwd_d128(Args a) {
     // so that LDS latency overlaps the products instead of stalling each
     // pair of them
     auto qk = [&](const lds_t *ks_, f32x16 &s0, f32x16 &s1) __attribute__((always_inline)) {
-        constexpr int kKPre = KR ? KD_FA_KPRE_KR : KD_FA_KPRE;
+        constexpr int kKPre = KR ? 0 : kKPreDma;
         s0 = (f32x16){};
         s1 = (f32x16){};
         vec8 ka[8][2];
@@ -459,7 +432,7 @@ void fa_fwd_d128(Args a) {
             s0 = E::mfma(ka[ks][0], qf[ks], s0);
             s1 = E::mfma(ka[ks][1], qf[ks], s1);
         }
-        if constexpr (KR ? KD_FA_SCHED_KR : KD_FA_SCHED) sched_qk<kKPre>();
+        if constexpr (!KR) sched_qk<kKPre>();
     };
 
     // the running max of a row moves to mx when `up` (a decision per row, so
@@ -592,12 +565,10 @@ void fa_fwd_d128(Args a) {
             sum = pack_sum(p, pb);
         }
         l_half += sum;
-        KD_FA_PRIO(1);
         pv(vs_, pb);
-        KD_FA_PRIO(0);
     };
 
-    if constexpr (!HAS_MASK && !KR && KD_FA_PIPE) {
+    if constexpr (!HAS_MASK && !KR) {
         // Pipelined: while step t computes the softmax of tile t, the same
         // wave issues the S^T products of tile t+1 between its VALU
         // instructions; the PV products of tile t follow.  K is staged one
@@ -628,7 +599,7 @@ void fa_fwd_d128(Args a) {
                          __attribute__((always_inline)) {
             constexpr bool NEXT = decltype(next_c)::value;
             constexpr bool TAIL = decltype(tail_c)::value;
-            constexpr int kKPre = KD_FA_KPRE;
+            constexpr int kKPre = kKPreDma;
             if (NEXT) {
                 issue_v(t + 1, dV);
                 if (t + 2 < n_tiles) issue_k(t + 2, dK);
@@ -672,7 +643,7 @@ void fa_fwd_d128(Args a) {
             }
             drop_tail(p);
             float sum = pack_sum(p, pb);
-            if (NEXT) sched_pipe<kKPre, KD_FA_PIPE_VPM>();
+            if (NEXT) sched_pipe<kKPre, kPipeVpm>();
             const float pair = pair_sum(sum);
             // the weight sum left [0, E::kSumCap]: exact max, rescale, redo
             if (__builtin_amdgcn_ballot_w64(!(pair <= E::kSumCap)) != 0) {
@@ -731,9 +702,7 @@ void fa_fwd_d128(Args a) {
                 if (KR) rope_load(t + 1);
             }
             f32x16 s0, s1;
-            KD_FA_PRIO(1);
             qk(ks_, s0, s1);
-            KD_FA_PRIO(0);
             soft_pv(tail_c, t * kBN, s0, s1, vs_);
             if (KR && has_next) rope_store(nK);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1050,7 +1019,7 @@ void fa_fwd_xres(Args a) {
     };
 
     auto qk = [&](const lds_t *ks_, f32x16 &s0, f32x16 &s1) __attribute__((always_inline)) {
-        constexpr int kKPre = HAS_MASK ? 1 : KD_FA_KPRE;
+        constexpr int kKPre = HAS_MASK ? 1 : kKPreDma;
         s0 = (f32x16){};
         s1 = (f32x16){};
         int ln = lane;
@@ -1070,7 +1039,7 @@ void fa_fwd_xres(Args a) {
             s0 = E::mfma(ka[ks][0], qf[ks], s0);
             s1 = E::mfma(ka[ks][1], qf[ks], s1);
         }
-        if constexpr (KD_FA_SCHED) sched_qk<kKPre>();
+        sched_qk<kKPre>();
     };
     auto move_max = [&](float mx, bool up) __attribute__((always_inline)) {   // fa_fwd_d128's rules, per row
         if (__builtin_amdgcn_ballot_w64(up) != 0) {
@@ -1705,26 +1674,31 @@ hipError_t launch(const Args &a, int kv_type, bool k_rope, int waves, hipStream_
 }
 
 // ---------------------------------------------------------------------------
-// K pre-pass of the workspace entry points: ops::rms_norm (kn_w) and
+// Pre-pass of the workspace entry points: ops::rms_norm (kn_w) and
 // rope::apply (src/rope.hpp:109-155) on K with the same F32 arithmetic as the
-// in-kernel transform, rounded to K's type, written in the operand type T (K
-// may be stored in F32) to out + key * o.key + head * o.head + batch *
-// o.batch: a contiguous [D, Lk, Hkv, Bk] workspace, or rows of the call's
-// own output buffer that the attention writes later (the staged path).
-// One thread per 8-element chunk; the 16 chunks of a row are 16 consecutive
-// lanes, which reduce the row's squares together.
+// in-kernel transform, rounded to the operand type T (K may be stored in
+// F32), written to out + key * o.key + head * o.head + batch * o.batch: a
+// contiguous [D, Lk, Hkv, Bk] workspace, or rows of the call's own output
+// buffer that the attention writes later (the staged path).  In the same
+// pass, an F32 V (the projection output ops::attention casts,
+// src/core/ops.hpp:168-169) is rounded to T into vout.  One thread per
+// 8-element chunk; the 16 chunks of a row are 16 consecutive lanes, which
+// reduce the row's squares together.
 // ---------------------------------------------------------------------------
 template <typename T, int RM, int kRopeKPairs>
-__global__ __launch_bounds__(256) void rope_k_kernel(Args a, char *out, KStrides o, int n_hb) {
+__global__ __launch_bounds__(256) void rope_k_kernel(Args a, char *out, KStrides o, char *vout, KStrides vo,
+                                                     int n_hb) {
     typedef Elem<T> E;
-    const int hk = a.H / a.rk2;   // K heads
+    // heads of the (b, h) pairs: K's, or V's in a pass that casts V only
+    // (when both are written, K and V have the same heads and batches)
+    const int nh = out ? a.H / a.rk2 : a.H / a.rv2;
     // x: 16 keys per workgroup, 16 lanes per key (one 16-byte output chunk
     // each); y: groups of kRopeKPairs (b, h) pairs (1 or 4), uniform per workgroup
     // (no division per chunk).  The chunk's rotation pairs and norm weights
-    // are the same for every (b, h): loaded once.  The group's K chunks are
-    // loaded before any is used, branch-free (both 16-byte halves of an F32
-    // chunk, or the 16-bit chunk twice; past the last pair, the last pair
-    // again, not stored).
+    // are the same for every (b, h): loaded once.  The group's K (and V)
+    // chunks are loaded before any is used, branch-free (both 16-byte halves
+    // of an F32 chunk, or the 16-bit chunk twice; past the last pair, the
+    // last pair again, not stored).
     const int key = (int)blockIdx.x * 16 + (int)(threadIdx.x >> 4);
     const int c = (int)(threadIdx.x & 15);
     if (key >= a.Lk) return;
@@ -1743,59 +1717,91 @@ __global__ __launch_bounds__(256) void rope_k_kernel(Args a, char *out, KStrides
         wn1 = *reinterpret_cast<const f32x4 *>(a.kn_w + c * 8 + 4);
     }
     const char *const kkey = a.k + (int64_t)key * a.k_nb1 + (k32 ? c * 32 : c * 16);
+    const char *const vkey = a.v + (int64_t)key * a.v_nb1 + c * 32;
     for (int g0 = (int)blockIdx.y * kRopeKPairs; g0 < n_hb; g0 += (int)gridDim.y * kRopeKPairs) {
-        u32x4 ra[kRopeKPairs], rb[kRopeKPairs];
+        u32x4 ra[kRopeKPairs], rb[kRopeKPairs], va[kRopeKPairs], vb[kRopeKPairs];
+        if (out) {
 #pragma unroll
-        for (int i = 0; i < kRopeKPairs; ++i) {
-            const int hb = min(g0 + i, n_hb - 1);
-            const char *src = kkey + (int64_t)(hb % hk) * a.k_nb2 + (int64_t)(hb / hk) * a.k_nb3;
-            ra[i] = ld16(src);
-            rb[i] = ld16(src + (k32 ? 16 : 0));
-        }
-#pragma unroll
-        for (int i = 0; i < kRopeKPairs; ++i) {
-            const int hb = g0 + i;
-            if (hb >= n_hb) break;
-            float x[8];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t w16 = ra[i][j];
-                const float lo16 = kbf ? bf16_lo(w16) : f16_lo(w16);
-                const float hi16 = kbf ? bf16_hi(w16) : f16_hi(w16);
-                const float e0 = __uint_as_float(j < 2 ? ra[i][2 * j] : rb[i][2 * j - 4]);
-                const float e1 = __uint_as_float(j < 2 ? ra[i][2 * j + 1] : rb[i][2 * j - 3]);
-                x[2 * j] = k32 ? e0 : lo16;
-                x[2 * j + 1] = k32 ? e1 : hi16;
+            for (int i = 0; i < kRopeKPairs; ++i) {
+                const int hb = min(g0 + i, n_hb - 1);
+                const char *src = kkey + (int64_t)(hb % nh) * a.k_nb2 + (int64_t)(hb / nh) * a.k_nb3;
+                ra[i] = ld16(src);
+                rb[i] = ld16(src + (k32 ? 16 : 0));
             }
-            if (knorm) rms_apply8(x, rms_scale(sum16_f64(sum_sq8(x)), a.norm_eps), wn0, wn1);
-            if (RM != KD_FA_ROPE_NONE) rotate8(x, cs0, cs1);
-            u32x4 w;
-            for (int e = 0; e < 4; ++e) w[e] = E::pack2(x[2 * e], x[2 * e + 1]);
-            *reinterpret_cast<u32x4 *>(out + (int64_t)key * o.key + (int64_t)(hb % hk) * o.head +
-                                       (int64_t)(hb / hk) * o.batch + c * 16) = w;
+        }
+        if (vout) {
+#pragma unroll
+            for (int i = 0; i < kRopeKPairs; ++i) {
+                const int hb = min(g0 + i, n_hb - 1);
+                const char *src = vkey + (int64_t)(hb % nh) * a.v_nb2 + (int64_t)(hb / nh) * a.v_nb3;
+                va[i] = ld16(src);
+                vb[i] = ld16(src + 16);
+            }
+        }
+        if (out) {
+#pragma unroll
+            for (int i = 0; i < kRopeKPairs; ++i) {
+                const int hb = g0 + i;
+                if (hb >= n_hb) break;
+                float x[8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t w16 = ra[i][j];
+                    const float lo16 = kbf ? bf16_lo(w16) : f16_lo(w16);
+                    const float hi16 = kbf ? bf16_hi(w16) : f16_hi(w16);
+                    const float e0 = __uint_as_float(j < 2 ? ra[i][2 * j] : rb[i][2 * j - 4]);
+                    const float e1 = __uint_as_float(j < 2 ? ra[i][2 * j + 1] : rb[i][2 * j - 3]);
+                    x[2 * j] = k32 ? e0 : lo16;
+                    x[2 * j + 1] = k32 ? e1 : hi16;
+                }
+                if (knorm) rms_apply8(x, rms_scale(sum16_f64(sum_sq8(x)), a.norm_eps), wn0, wn1);
+                if (RM != KD_FA_ROPE_NONE) rotate8(x, cs0, cs1);
+                u32x4 w;
+                for (int e = 0; e < 4; ++e) w[e] = E::pack2(x[2 * e], x[2 * e + 1]);
+                *reinterpret_cast<u32x4 *>(out + (int64_t)key * o.key + (int64_t)(hb % nh) * o.head +
+                                           (int64_t)(hb / nh) * o.batch + c * 16) = w;
+            }
+        }
+        if (vout) {
+#pragma unroll
+            for (int i = 0; i < kRopeKPairs; ++i) {
+                const int hb = g0 + i;
+                if (hb >= n_hb) break;
+                u32x4 w;
+                w[0] = E::pack2(__uint_as_float(va[i][0]), __uint_as_float(va[i][1]));
+                w[1] = E::pack2(__uint_as_float(va[i][2]), __uint_as_float(va[i][3]));
+                w[2] = E::pack2(__uint_as_float(vb[i][0]), __uint_as_float(vb[i][1]));
+                w[3] = E::pack2(__uint_as_float(vb[i][2]), __uint_as_float(vb[i][3]));
+                *reinterpret_cast<u32x4 *>(vout + (int64_t)key * vo.key + (int64_t)(hb % nh) * vo.head +
+                                           (int64_t)(hb / nh) * vo.batch + c * 16) = w;
+            }
         }
     }
 }
 
 template <typename T, int P>
-static void launch_rope_k_p(const Args &a, dim3 grid, char *o, const KStrides &st, int n_hb, hipStream_t stream) {
-    switch (a.rope_mode) {
+static void launch_rope_k_p(const Args &a, dim3 grid, char *o, const KStrides &st, char *vo, const KStrides &vst,
+                            int n_hb, hipStream_t stream) {
+    switch (o ? a.rope_mode : KD_FA_ROPE_NONE) {   // a V-only pass rotates nothing
     case KD_FA_ROPE_TABLE:
-        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_TABLE, P>), grid, dim3(256), 0, stream, a, o, st, n_hb);
+        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_TABLE, P>), grid, dim3(256), 0, stream, a, o, st, vo, vst,
+                           n_hb);
         break;
     case KD_FA_ROPE_AXES:
-        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_AXES, P>), grid, dim3(256), 0, stream, a, o, st, n_hb);
+        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_AXES, P>), grid, dim3(256), 0, stream, a, o, st, vo, vst,
+                           n_hb);
         break;
     default:
-        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_NONE, P>), grid, dim3(256), 0, stream, a, o, st, n_hb);
+        hipLaunchKernelGGL((rope_k_kernel<T, KD_FA_ROPE_NONE, P>), grid, dim3(256), 0, stream, a, o, st, vo, vst,
+                           n_hb);
         break;
     }
 }
 
-hipError_t launch_rope_k(const Args &a, int kv_type, int k_heads, int k_batch, void *out, const KStrides &st,
-                         hipStream_t stream) {
-    const int64_t n_hb = (int64_t)k_heads * k_batch;
-    if (a.Lk == 0 || n_hb == 0) return hipSuccess;
+hipError_t launch_rope_k(const Args &a, int kv_type, int heads, int batch, void *out, const KStrides &st,
+                         void *vout, const KStrides &vst, hipStream_t stream) {
+    const int64_t n_hb = (int64_t)heads * batch;
+    if (a.Lk == 0 || n_hb == 0 || (!out && !vout)) return hipSuccess;
     // x: 16 keys per workgroup; y: groups of P (b, h) pairs, at most 65,535
     // (a workgroup takes every gridDim.y-th group beyond that).  P = 4 --
     // the rotation pairs loaded once for four heads, four loads in flight
@@ -1807,12 +1813,13 @@ hipError_t launch_rope_k(const Args &a, int kv_type, int k_heads, int k_batch, v
     const int64_t n_g = (n_hb + P - 1) / P;
     const dim3 grid((unsigned)nx, (unsigned)(n_g < 65535 ? n_g : 65535));
     char *o = static_cast<char *>(out);
+    char *vo = static_cast<char *>(vout);
     if (kv_type == KD_FA_TYPE_BF16) {
-        if (P == 4) launch_rope_k_p<__bf16, 4>(a, grid, o, st, (int)n_hb, stream);
-        else launch_rope_k_p<__bf16, 1>(a, grid, o, st, (int)n_hb, stream);
+        if (P == 4) launch_rope_k_p<__bf16, 4>(a, grid, o, st, vo, vst, (int)n_hb, stream);
+        else launch_rope_k_p<__bf16, 1>(a, grid, o, st, vo, vst, (int)n_hb, stream);
     } else {
-        if (P == 4) launch_rope_k_p<_Float16, 4>(a, grid, o, st, (int)n_hb, stream);
-        else launch_rope_k_p<_Float16, 1>(a, grid, o, st, (int)n_hb, stream);
+        if (P == 4) launch_rope_k_p<_Float16, 4>(a, grid, o, st, vo, vst, (int)n_hb, stream);
+        else launch_rope_k_p<_Float16, 1>(a, grid, o, st, vo, vst, (int)n_hb, stream);
     }
     return hipGetLastError();
 }

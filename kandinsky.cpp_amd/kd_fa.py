@@ -11,8 +11,8 @@ Tensors are torch tensors whose shape is ggml's ``ne`` reversed, so the
 ggml view ``[ne0, ne1, ne2, ne3]`` is the torch shape ``(ne3, ne2, ne1, ne0)``:
 
     q    (B,  H,   Lq,  Dk)   float32 / float16 / bfloat16
-    k    (Bk, Hkv, Lk,  Dk)   float16 / bfloat16
-    v    (Bk, Hkv, Lk,  Dv)   same dtype as k
+    k    (Bk, Hkv, Lk,  Dk)   float16 / bfloat16 (float32 in the workspace forms)
+    v    (Bk, Hkv, Lk,  Dv)   same dtype as k (float32 in the workspace forms)
     mask (Bm, Hm,  Lq', Lk')  float16, optional
     dst  (B,  Lq,  H,   Dv)   float32   (ggml's permuted [Dv, H, Lq, B])
 
@@ -51,6 +51,8 @@ ERR_LAUNCH = -7
 ERR_DEVICE = -8
 ERR_SCRATCH = -9
 STATIC_SCRATCH_BYTES = 64 << 20
+# layout version of the structs below (KD_FA_ABI_VERSION in include/kd_fa.h)
+ABI_VERSION = 3
 
 # kd_fa_set_routing flags (comparison hooks for tests and tuning)
 ROUTE_DEFAULT = 0
@@ -88,6 +90,7 @@ class KdFaDesc(ctypes.Structure):
         ("max_bias", ctypes.c_float),
         ("logit_softcap", ctypes.c_float),
         ("prec", ctypes.c_int32),
+        ("cast_type", ctypes.c_int32),
     ]
 
 
@@ -171,6 +174,11 @@ def _lib():
         lib.kd_fa_dit_run_static.restype = ctypes.c_int
         lib.kd_fa_set_routing.argtypes = [ctypes.c_int]
         lib.kd_fa_set_routing.restype = ctypes.c_int
+        lib.kd_fa_abi_version.argtypes = []
+        lib.kd_fa_abi_version.restype = ctypes.c_int
+        if lib.kd_fa_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} lays out its structs as ABI version {lib.kd_fa_abi_version()}, "
+                               f"this binding as {ABI_VERSION}: rebuild the library")
         _LIB = lib
     return _LIB
 
@@ -247,7 +255,10 @@ def view(t) -> KdFaTensor:
     return d
 
 
-def make_desc(q, k, v, mask, dst, scale, max_bias=0.0, logit_softcap=0.0, prec=PREC_F32) -> KdFaDesc:
+def make_desc(q, k, v, mask, dst, scale, max_bias=0.0, logit_softcap=0.0, prec=PREC_F32, cast_type=0) -> KdFaDesc:
+    """The node over torch tensors.  ``cast_type``: the type an F32 K / V is
+    cast to by the workspace forms (0 or TYPE_F16: ggml_cast to F16, as
+    ops::attention does; TYPE_BF16)."""
     d = KdFaDesc()
     d._keep = (q, k, v, mask, dst)  # the struct holds raw pointers: keep the tensors alive
     d.q, d.k, d.v = view(q), view(k), view(v)
@@ -257,6 +268,7 @@ def make_desc(q, k, v, mask, dst, scale, max_bias=0.0, logit_softcap=0.0, prec=P
     d.max_bias = float(max_bias)
     d.logit_softcap = float(logit_softcap)
     d.prec = int(prec)
+    d.cast_type = int(cast_type)
     return d
 
 
@@ -371,32 +383,36 @@ def run_static(desc: KdFaDesc, rope: KdFaRope | None = None, norm: KdFaQkNorm | 
 
 
 def workspace_size(desc: KdFaDesc) -> int:
-    """kd_fa_rope_workspace_size: bytes of K-sized buffer for kd_fa_rope_run_ws."""
+    """kd_fa_rope_workspace_size: bytes of workspace kd_fa_rope_run_ws needs
+    (the rotated K, and the cast V when V is float32)."""
     return int(_lib().kd_fa_rope_workspace_size(ctypes.byref(desc)))
 
 
 def workspace_size_full(desc: KdFaDesc, rope: KdFaRope | None = None, norm: KdFaQkNorm | None = None) -> int:
     """kd_fa_workspace_size: bytes of workspace the node can use (the
-    transformed K, then the mask summary of a masked short-key node)."""
+    transformed K, the cast V, then the mask summary of a masked short-key
+    node)."""
     return int(_lib().kd_fa_workspace_size(ctypes.byref(desc), ctypes.byref(rope) if rope is not None else None,
                                            ctypes.byref(norm) if norm is not None else None))
 
 
 def flash_attn_ext(q, k, v, mask=None, scale=None, max_bias=0.0, logit_softcap=0.0,
-                   dst=None, rope=None, stream=None, workspace=None, norm=None, out_dtype=None):
+                   dst=None, rope=None, stream=None, workspace=None, norm=None, out_dtype=None, cast_type=0):
     """GGML_OP_FLASH_ATTN_EXT on the GPU; returns dst (B, Lq, H, Dv).
 
     ``rope`` is a KdFaRope (rope_table / rope_axes) to rotate Q and K on load;
     ``norm`` a KdFaQkNorm (qk_norm) to RMS-normalise them first
     (kd_fa_dit_run).  dst defaults to float32 (the node's type); ``out_dtype``
-    torch.bfloat16 / torch.float16 stores O rounded instead.  Raises
-    KdFaError on any non-zero status (nothing is enqueued then)."""
+    torch.bfloat16 / torch.float16 stores O rounded instead.  float32 K / V
+    (with a workspace, through ``norm`` or ``rope``) are cast to ``cast_type``
+    by the pre-pass.  Raises KdFaError on any non-zero status (nothing is
+    enqueued then)."""
     torch = _torch()
     if scale is None:
         scale = 1.0 / float(q.shape[-1]) ** 0.5
     if dst is None:
         dst = torch.empty(out_shape(q, v), dtype=out_dtype or torch.float32, device=q.device)
-    d = make_desc(q, k, v, mask, dst, scale, max_bias, logit_softcap)
+    d = make_desc(q, k, v, mask, dst, scale, max_bias, logit_softcap, cast_type=cast_type)
     st = run_desc(d, rope, stream, workspace, norm)
     if st != OK:
         name = "kd_fa_dit_run" if norm is not None else "kd_fa_rope_run" if rope is not None else "kd_fa_run"

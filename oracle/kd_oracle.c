@@ -12,6 +12,7 @@
 #define _GNU_SOURCE
 #include "kd_oracle.h"
 
+#include <immintrin.h>
 #include <math.h>
 #include <pthread.h>
 #include <stdlib.h>
@@ -97,6 +98,56 @@ void kdo_f16_to_f32_n(const uint16_t *s, float *d, int64_t n) {
 }
 void kdo_bf16_to_f32_n(const uint16_t *s, float *d, int64_t n) {
     for (int64_t i = 0; i < n; ++i) d[i] = kdo_bf16_to_f32(s[i]);
+}
+
+/* The same two conversions by the F16C instructions (VCVTPS2PH with
+ * round-to-nearest-even, VCVTPH2PS), eight lanes at a time, as ggml's SIMD
+ * paths convert; pinned bitwise against the software codec above
+ * (kdo_f16_codec_mismatches). */
+void kdo_f32_to_f16_hw_n(const float *s, uint16_t *d, int64_t n) {
+    int64_t i = 0;
+    for (; i + 8 <= n; i += 8)
+        _mm_storeu_si128((__m128i *)(d + i),
+                         _mm256_cvtps_ph(_mm256_loadu_ps(s + i), _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC));
+    for (; i < n; ++i)
+        d[i] = (uint16_t)_mm_extract_epi16(_mm_cvtps_ph(_mm_set_ss(s[i]), _MM_FROUND_TO_NEAREST_INT), 0);
+}
+void kdo_f16_to_f32_hw_n(const uint16_t *s, float *d, int64_t n) {
+    int64_t i = 0;
+    for (; i + 8 <= n; i += 8) _mm256_storeu_ps(d + i, _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(s + i))));
+    for (; i < n; ++i) d[i] = _mm_cvtss_f32(_mm_cvtph_ps(_mm_cvtsi32_si128(s[i])));
+}
+
+/* Mismatches between the F16C and the software conversions: every F16 bit
+ * pattern decoded, and `count` F32 bit patterns start, start + stride, ...
+ * encoded (NaN payloads included; VCVTPH2PS quiets a signalling NaN, so a
+ * decoded NaN is compared with its quiet bit set). */
+int64_t kdo_f16_codec_mismatches(uint32_t start, uint32_t stride, int64_t count) {
+    pthread_once(&g_f16_once, f16_table_init);
+    int64_t bad = 0;
+    uint16_t h[8];
+    float f[8];
+    for (uint32_t i = 0; i < 65536; i += 8) {
+        for (int l = 0; l < 8; ++l) h[l] = (uint16_t)(i + l);
+        kdo_f16_to_f32_hw_n(h, f, 8);
+        for (int l = 0; l < 8; ++l) {
+            const uint32_t hw = f32_bits(f[l]), sw = f32_bits(f16_decode(h[l]));
+            const int nan = (sw & 0x7fffffffu) > 0x7f800000u;
+            bad += nan ? hw != (sw | 0x00400000u) : hw != sw;
+        }
+    }
+    uint32_t x = start;
+    for (int64_t i = 0; i < count; i += 8) {
+        const int m = count - i < 8 ? (int)(count - i) : 8;
+        uint32_t u[8];
+        for (int l = 0; l < m; ++l, x += stride) {
+            u[l] = x;
+            f[l] = bits_f32(x);
+        }
+        kdo_f32_to_f16_hw_n(f, h, m);
+        for (int l = 0; l < m; ++l) bad += h[l] != kdo_f32_to_f16(bits_f32(u[l]));
+    }
+    return bad;
 }
 
 static inline float load_elem(const char *p, int type) {
@@ -325,14 +376,16 @@ static inline void row_coords(const kd_fa_desc *d, int64_t ir, int64_t *b, int64
     *i = ir - *b * H * Lq - *h * Lq;
 }
 
-/* K and V of one (b_kv, h_kv) head converted to float once; K rotated
- * and rounded to its own type when RoPE is on. */
+/* K of one (b_k, h_k) head and V of one (b_v, h_v) head converted to
+ * float once (ggml broadcasts K and V separately: h_k = h / (H / Hk),
+ * h_v = h / (H / Hv)); K rotated and rounded to its own type when RoPE is
+ * on. */
 typedef struct {
-    int64_t bk, hk;
+    int64_t bk, hk, bv, hv;
     float *kf, *vf;
 } kv_cache;
 
-static void load_kv(const fa_job *j, kv_cache *c, int64_t bk, int64_t hk) {
+static void load_kv(const fa_job *j, kv_cache *c, int64_t bk, int64_t hk, int64_t bv, int64_t hv) {
     const kd_fa_desc *d = j->d;
     const int64_t Dk = d->k.ne[0], Dv = d->v.ne[0], Lk = d->k.ne[1];
     const int rope = j->r && j->r->mode != KD_FA_ROPE_NONE;
@@ -344,12 +397,14 @@ static void load_kv(const fa_job *j, kv_cache *c, int64_t bk, int64_t hk) {
             rope_row(j->r, jx, kr, Dk);
             for (int64_t e = 0; e < Dk; ++e) kr[e] = kdo_round_to(kr[e], d->k.type);
         }
-        const char *vp = (const char *)d->v.data + jx * d->v.nb[1] + hk * d->v.nb[2] + bk * d->v.nb[3];
+        const char *vp = (const char *)d->v.data + jx * d->v.nb[1] + hv * d->v.nb[2] + bv * d->v.nb[3];
         float *vr = c->vf + jx * Dv;
         for (int64_t e = 0; e < Dv; ++e) vr[e] = load_elem(vp + e * d->v.nb[0], d->v.type);
     }
     c->bk = bk;
     c->hk = hk;
+    c->bv = bv;
+    c->hv = hv;
 }
 
 /* ggml_vec_dot_{f16,bf16} with F32 lanes: 32 running FMA sums, combined
@@ -371,12 +426,13 @@ static void run_rows(fa_job *j, int64_t r0, int64_t r1) {
     const int64_t Dk = d->k.ne[0], Dv = d->v.ne[0], Lk = d->k.ne[1];
     const int64_t H = d->q.ne[2], B = d->q.ne[3];
     const int64_t rk2 = H / d->k.ne[2], rk3 = B / d->k.ne[3];
+    const int64_t rv2 = H / d->v.ne[2], rv3 = B / d->v.ne[3];
     const int vt = d->v.type;
     const float scale = d->scale, softcap = d->logit_softcap;
     const int rope = j->r && j->r->mode != KD_FA_ROPE_NONE;
 
     kv_cache c;
-    c.bk = c.hk = -1;
+    c.bk = c.hk = c.bv = c.hv = -1;
     c.kf = (float *)malloc(sizeof(float) * (size_t)(Lk * Dk + 1));
     c.vf = (float *)malloc(sizeof(float) * (size_t)(Lk * Dv + 1));
     float *q = (float *)malloc(sizeof(float) * (size_t)Dk);
@@ -389,8 +445,8 @@ static void run_rows(fa_job *j, int64_t r0, int64_t r1) {
         const int64_t ir = j->order[x];
         int64_t b, h, i;
         row_coords(d, ir, &b, &h, &i);
-        const int64_t bk = b / rk3, hk = h / rk2;
-        if (bk != c.bk || hk != c.hk) load_kv(j, &c, bk, hk);
+        const int64_t bk = b / rk3, hk = h / rk2, bv = b / rv3, hv = h / rv2;
+        if (bk != c.bk || hk != c.hk || bv != c.bv || hv != c.hv) load_kv(j, &c, bk, hk, bv, hv);
 
         /* Q row -> F32 -> (RoPE) -> K's dot type. */
         const char *qp = (const char *)d->q.data + i * d->q.nb[1] + h * d->q.nb[2] + b * d->q.nb[3];
@@ -424,8 +480,15 @@ static void run_rows(fa_job *j, int64_t r0, int64_t r1) {
                     M = s;
                     ms = expf(Mold - M);
                     if (f16acc) {
-                        for (int64_t e = 0; e < Dv; ++e)
-                            vkq16[e] = kdo_f32_to_f16(f16_to_f32(vkq16[e]) * ms);
+                        /* ggml_vec_scale_f16: F16 -> F32, product, -> F16 */
+                        int64_t e = 0;
+                        const __m256 vm = _mm256_set1_ps(ms);
+                        for (; e + 8 <= Dv; e += 8) {
+                            const __m256 a = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(vkq16 + e)));
+                            _mm_storeu_si128((__m128i *)(vkq16 + e),
+                                             _mm256_cvtps_ph(_mm256_mul_ps(a, vm), _MM_FROUND_TO_NEAREST_INT));
+                        }
+                        for (; e < Dv; ++e) vkq16[e] = kdo_f32_to_f16(f16_to_f32(vkq16[e]) * ms);
                     } else {
                         for (int64_t e = 0; e < Dv; ++e) vkq32[e] *= ms;
                     }
@@ -433,8 +496,16 @@ static void run_rows(fa_job *j, int64_t r0, int64_t r1) {
                     vs = expf(s - M);
                 }
                 if (f16acc) {
-                    for (int64_t e = 0; e < Dv; ++e)
-                        vkq16[e] = kdo_f32_to_f16(fmaf(v[e], vs, f16_to_f32(vkq16[e])));
+                    /* ggml_vec_mad_f16: one fused multiply-add per element,
+                     * the F16 accumulator converted by F16C both ways */
+                    int64_t e = 0;
+                    const __m256 vv = _mm256_set1_ps(vs);
+                    for (; e + 8 <= Dv; e += 8) {
+                        const __m256 a = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(vkq16 + e)));
+                        const __m256 r = _mm256_fmadd_ps(_mm256_loadu_ps(v + e), vv, a);
+                        _mm_storeu_si128((__m128i *)(vkq16 + e), _mm256_cvtps_ph(r, _MM_FROUND_TO_NEAREST_INT));
+                    }
+                    for (; e < Dv; ++e) vkq16[e] = kdo_f32_to_f16(fmaf(v[e], vs, f16_to_f32(vkq16[e])));
                 } else {
                     for (int64_t e = 0; e < Dv; ++e) vkq32[e] = fmaf(v[e], vs, vkq32[e]);
                 }

@@ -64,6 +64,15 @@ void kdo_rope_apply_f32(const float *x, int64_t D, int64_t H, int64_t L,
 void kdo_rms_norm_mul(const float *x, int64_t rows, int64_t D, const float *w,
                       float eps, float *out);
 
+/* F16C (VCVTPS2PH round-to-nearest-even / VCVTPH2PS) forms of the F16
+ * conversions, used by kdo_fa_ggml's F16 V accumulator as ggml's SIMD paths
+ * convert; kdo_f16_codec_mismatches counts where they differ from the
+ * software codec: all 65,536 F16 patterns decoded, and `count` F32 bit
+ * patterns from `start` in steps of `stride` encoded. */
+void kdo_f32_to_f16_hw_n(const float *src, uint16_t *dst, int64_t n);
+void kdo_f16_to_f32_hw_n(const uint16_t *src, float *dst, int64_t n);
+int64_t kdo_f16_codec_mismatches(uint32_t start, uint32_t stride, int64_t count);
+
 static inline int64_t kdo_row_id(int64_t b, int64_t h, int64_t i,
                                  int64_t H, int64_t Lq) {
     return i + Lq * (h + H * b);

@@ -33,7 +33,7 @@ class Tensor(ctypes.Structure):
 class Desc(ctypes.Structure):
     _fields_ = [("q", Tensor), ("k", Tensor), ("v", Tensor), ("mask", Tensor), ("sinks", Tensor), ("dst", Tensor),
                 ("scale", ctypes.c_float), ("max_bias", ctypes.c_float),
-                ("logit_softcap", ctypes.c_float), ("prec", ctypes.c_int32)]
+                ("logit_softcap", ctypes.c_float), ("prec", ctypes.c_int32), ("cast_type", ctypes.c_int32)]
 
 
 class Rope(ctypes.Structure):
@@ -68,6 +68,10 @@ def lib():
             getattr(L, name).argtypes = [fp, P(ctypes.c_uint16), ctypes.c_int64]
         for name in ("kdo_f16_to_f32_n", "kdo_bf16_to_f32_n"):
             getattr(L, name).argtypes = [P(ctypes.c_uint16), fp, ctypes.c_int64]
+        L.kdo_f32_to_f16_hw_n.argtypes = [fp, P(ctypes.c_uint16), ctypes.c_int64]
+        L.kdo_f16_to_f32_hw_n.argtypes = [P(ctypes.c_uint16), fp, ctypes.c_int64]
+        L.kdo_f16_codec_mismatches.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int64]
+        L.kdo_f16_codec_mismatches.restype = ctypes.c_int64
         L.kdo_rope_freqs.argtypes = [ctypes.c_int, ctypes.c_float, fp]
         L.kdo_rope_text_table.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_float, fp]
         L.kdo_rope_visual_table.argtypes = [ctypes.c_int] * 3 + [ip, fp, ctypes.c_float, fp]
@@ -228,6 +232,20 @@ def f32_to_f16_bits(a):
     lib().kdo_f32_to_f16_n(a.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
                            out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), a.size)
     return out
+
+
+def f32_to_f16_bits_hw(a):
+    """f32_to_f16_bits by the F16C instruction (the CPU baseline's path)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.uint16)
+    lib().kdo_f32_to_f16_hw_n(a.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                              out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), a.size)
+    return out
+
+
+def f16_codec_mismatches(start, stride, count):
+    """Where the F16C and software F16 conversions differ (see kd_oracle.h)."""
+    return int(lib().kdo_f16_codec_mismatches(start, stride, count))
 
 
 def f32_to_bf16_bits(a):

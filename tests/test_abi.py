@@ -316,18 +316,21 @@ def test_norm_descriptor_checks():
     assert ask(kd_fa.qk_norm(w[:128], w[:128], -1.0)) == (False, kd_fa.ERR_ROPE)
 
 
-def test_f32_k_supports_agrees_with_run():
-    """kd_fa_dit_supports accepts an F32 K (the projection output) only when K
-    is transformed -- normalised or rotated -- and kd_fa_dit_run then needs
-    the workspace whose pre-pass rounds it; both answers are given before
-    any device work, so they are checked here on the host."""
+def test_f32_k_v_supports_agrees_with_run():
+    """kd_fa_dit_supports answers for the workspace form, whose pre-pass
+    casts an F32 K and V (the projection outputs ops::attention receives,
+    src/core/ops.hpp:167-169): it accepts them with or without a K transform,
+    and kd_fa_dit_run without a workspace names the missing buffer.  The node
+    itself (kd_fa_supports, kd_fa_run, kd_fa_rope_run) keeps 16-bit K and V.
+    All answers come before any device work, so they are checked here on the
+    host."""
     q, k, v, m, dst = _node(Lq=60, Lk=60, qt=torch.float32, kt=torch.bfloat16)
-    k32 = k.float()
     w = torch.ones(128)
     lib = kd_fa.lib()
+    table = kd_fa.rope_table(torch.zeros((60, 128)))
 
-    def ask(rope, norm):
-        d = kd_fa.make_desc(q, k32, v, None, dst, 0.1)
+    def ask(kk, vv, rope, norm, cast_type=0):
+        d = kd_fa.make_desc(q, kk, vv, None, dst, 0.1, cast_type=cast_type)
         reason = ctypes.c_int(0)
         ok = lib.kd_fa_dit_supports(ctypes.byref(d), ctypes.byref(rope) if rope is not None else None,
                                     ctypes.byref(norm) if norm is not None else None, ctypes.byref(reason))
@@ -335,13 +338,64 @@ def test_f32_k_supports_agrees_with_run():
                                 ctypes.byref(norm) if norm is not None else None, None, 0, None)
         return bool(ok), reason.value, run
 
-    table = kd_fa.rope_table(torch.zeros((60, 128)))
-    # no K transform: F32 K is not an operand type of the node
-    assert ask(None, None) == (False, kd_fa.ERR_TYPE, kd_fa.ERR_TYPE)
-    assert ask(None, kd_fa.qk_norm(w, None)) == (False, kd_fa.ERR_TYPE, kd_fa.ERR_TYPE)
-    # K transformed: supported, and the run without a workspace says so
-    assert ask(table, None) == (True, 0, kd_fa.ERR_NULL)
-    assert ask(None, kd_fa.qk_norm(None, w)) == (True, 0, kd_fa.ERR_NULL)
+    k32, v32 = k.float(), v.float()
+    for kk, vv in ((k32, v), (k, v32), (k32, v32)):
+        assert ask(kk, vv, None, None) == (True, 0, kd_fa.ERR_NULL)
+        assert ask(kk, vv, table, None) == (True, 0, kd_fa.ERR_NULL)
+        assert ask(kk, vv, None, kd_fa.qk_norm(None, w)) == (True, 0, kd_fa.ERR_NULL)
+        assert ask(kk, vv, None, None, cast_type=kd_fa.TYPE_BF16) == (True, 0, kd_fa.ERR_NULL)
+        # the cast goes to a 16-bit type only
+        assert ask(kk, vv, None, None, cast_type=kd_fa.TYPE_F32 + 7)[:2] == (False, kd_fa.ERR_TYPE)
+        # the node and its no-workspace forms: 16-bit K and V
+        d = kd_fa.make_desc(q, kk, vv, None, dst, 0.1)
+        assert _sup(q, kk, vv, None, dst) == (False, kd_fa.ERR_TYPE)
+        assert lib.kd_fa_run(ctypes.byref(d), None) == kd_fa.ERR_TYPE
+        assert lib.kd_fa_rope_run(ctypes.byref(d), ctypes.byref(table), None) == kd_fa.ERR_TYPE
+    # K and V of different 16-bit types stay refused; cast_type is ignored then
+    assert ask(k, v.half(), None, None)[:2] == (False, kd_fa.ERR_TYPE)
+    assert ask(k, v, None, None, cast_type=99)[:2] == (True, 0)
+    # the D = 512 node has no cast pass
+    q5 = torch.zeros((1, 1, 64, 512), dtype=torch.float32)
+    k5 = torch.zeros((1, 1, 64, 512), dtype=torch.float32)
+    d5 = kd_fa.make_desc(q5, k5, k5, None, torch.zeros((1, 64, 1, 512)), 0.1)
+    reason = ctypes.c_int(0)
+    assert lib.kd_fa_dit_supports(ctypes.byref(d5), None, None, ctypes.byref(reason)) == 0
+    assert reason.value == kd_fa.ERR_TYPE
+
+
+def test_cast_workspace_sizes():
+    """Workspace layout of the cast operands: the transformed K, then (at a
+    256-byte boundary) the cast V, then the mask summary; an F32 K with no
+    transform still takes its K part (the cast)."""
+    lib = kd_fa.lib()
+    B, H, Lq, Lk = 2, 4, 64, 77
+    q = torch.zeros((B, H, Lq, 128), dtype=torch.float32)
+    k16 = torch.zeros((B, H, Lk, 128), dtype=torch.bfloat16)
+    k32, v32 = k16.float(), k16.float()
+    dst = torch.zeros((B, Lq, H, 128), dtype=torch.float32)
+    kb = B * H * Lk * 256
+    part = (kb + 255) // 256 * 256
+    m = torch.zeros((B, 1, Lq, 80), dtype=torch.float16)
+    summary = 4 * B * 1 * ((Lq + 31) // 32)
+
+    def full(kk, vv, mask=None, norm=None):
+        d = kd_fa.make_desc(q, kk, vv, mask, dst, 0.1)
+        return kd_fa.workspace_size_full(d, None, norm)
+
+    def rope_ws(kk, vv):
+        return kd_fa.workspace_size(kd_fa.make_desc(q, kk, vv, None, dst, 0.1))
+
+    assert full(k16, k16) == 0
+    assert full(k32, k16) == kb
+    assert full(k16, v32) == kb
+    assert full(k32, v32) == part + kb
+    assert full(k16, k16, norm=kd_fa.qk_norm(None, torch.ones(128))) == kb
+    assert full(k32, v32, mask=m) == part + part + summary
+    assert full(k16, k16, mask=m) == summary
+    assert rope_ws(k16, k16) == kb
+    assert rope_ws(k16, v32) == part + kb
+    assert rope_ws(k32, v32) == part + kb
+    assert lib.kd_fa_abi_version() == kd_fa.ABI_VERSION
 
 
 def test_routing_hook_round_trips():
@@ -367,13 +421,15 @@ def test_product_reads_no_environment():
             assert not re.search(r"\bgetenv\b|os\.environ", text), name
 
 
-def test_static_entry_point_refuses_oversize_k_before_device_work():
-    """kd_fa_dit_run_static checks the transformed K against its static
-    scratch (KD_FA_STATIC_SCRATCH_BYTES) on the host, before any device
-    call: a K one row over the limit is refused with KD_FA_ERR_SCRATCH, an
-    invalid node with its own reason."""
+def test_static_entry_point_refuses_oversize_f32_before_device_work():
+    """kd_fa_dit_run_static checks the transformed K and cast V against its
+    static scratch (KD_FA_STATIC_SCRATCH_BYTES) on the host, before any
+    device call: an F32 K or V one row over the limit is refused with
+    KD_FA_ERR_SCRATCH (their cast needs the workspace), an invalid node with
+    its own reason.  (A 16-bit K over the limit runs without the workspace:
+    a GPU test covers it.)"""
     lib = kd_fa.lib()
-    L = kd_fa.STATIC_SCRATCH_BYTES // (128 * 2) + 1          # one bf16 K row over
+    L = kd_fa.STATIC_SCRATCH_BYTES // (128 * 2) + 1          # one K row over
     q = torch.zeros((1, 1, 4, 128), dtype=torch.bfloat16)
     k = torch.zeros((1, 1, L, 128), dtype=torch.bfloat16)
     dst = torch.zeros((1, 4, 1, 128), dtype=torch.float32)
@@ -381,7 +437,9 @@ def test_static_entry_point_refuses_oversize_k_before_device_work():
     tab = torch.zeros((L, 128))
     rope = kd_fa.rope_table(tab)
     assert kd_fa.workspace_size(d) == kd_fa.STATIC_SCRATCH_BYTES + 256
-    assert lib.kd_fa_dit_run_static(ctypes.byref(d), ctypes.byref(rope), None, None) == kd_fa.ERR_SCRATCH
+    for kk, vv in ((k.float(), k), (k, k.float())):
+        d32 = kd_fa.make_desc(q, kk, vv, None, dst, 0.1)
+        assert lib.kd_fa_dit_run_static(ctypes.byref(d32), ctypes.byref(rope), None, None) == kd_fa.ERR_SCRATCH
     bad = kd_fa.make_desc(q, k, k, None, dst, 0.1, max_bias=1.0)
     assert lib.kd_fa_dit_run_static(ctypes.byref(bad), ctypes.byref(rope), None, None) == kd_fa.ERR_PARAM
     assert b"static scratch" in lib.kd_fa_strerror(kd_fa.ERR_SCRATCH)

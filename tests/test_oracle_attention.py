@@ -162,6 +162,27 @@ def test_gqa_and_batch_broadcast_equal_explicit_repeat():
     assert np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("f64", [True, False])
+def test_k_and_v_broadcast_separately(f64):
+    """ggml maps a query head to its K head and its V head separately
+    (h / (H / Hk), h / (H / Hv)); with 2 K heads and 4 V heads for H = 4, and
+    K over batch but V not, the result equals explicitly repeated operands."""
+    q, _, _ = qkv(2, 4, 6, 9, torch.float16, seed=19)
+    k = qkv(1, 2, 1, 9, torch.float16, seed=20)[1]
+    v = qkv(2, 4, 1, 9, torch.float16, seed=21)[2]
+    kr = k.repeat_interleave(2, dim=1).expand(2, -1, -1, -1).contiguous()
+    if f64:
+        assert np.array_equal(orc.fa_f64(q, k, v), orc.fa_f64(q, kr, v))
+    else:
+        a, _ = orc.fa_ggml(q, k, v)
+        b, _ = orc.fa_ggml(q, kr, v)
+        assert torch.equal(a, b)
+    # V indexed with the K head (V heads 0, 0, 1, 1 for query heads 0..3)
+    # gives another result
+    vw = v[:, :2].repeat_interleave(2, dim=1).contiguous()
+    assert not np.allclose(orc.fa_f64(q, k, v), orc.fa_f64(q, k, vw))
+
+
 def test_mask_broadcast_over_heads_and_rows_beyond_lq():
     q, k, v = qkv(2, 2, 5, 7, torch.bfloat16, seed=10)
     g = torch.Generator().manual_seed(3)

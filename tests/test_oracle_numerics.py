@@ -44,6 +44,23 @@ def test_f32_to_f16_round_to_nearest_even():
     assert np.array_equal(got, ref)
 
 
+def test_f16c_conversions_equal_software_codec():
+    """The F16C path of the CPU baseline's F16 accumulator: every F16
+    pattern decoded and every positive F32 pattern from 2^-26 (below half
+    the smallest F16 subnormal) to 2^17 (beyond the F16 overflow) encoded,
+    bit for bit equal to the software codec; negatives, NaN payloads,
+    infinities and the rest of the range on strided sweeps."""
+    lo, hi = 0x32800000, 0x48000000                 # 2^-26 .. 2^17
+    assert orc.f16_codec_mismatches(lo, 1, hi - lo) == 0
+    assert orc.f16_codec_mismatches(0x80000000 | lo, 1, (hi - lo) // 7 + 1) == 0
+    assert orc.f16_codec_mismatches(0, 4099, (1 << 32) // 4099) == 0
+    assert orc.f16_codec_mismatches(0x7f800000, 1, 1 << 16) == 0      # +inf, NaNs
+    assert orc.f16_codec_mismatches(0xff800000, 1, 1 << 16) == 0
+    x = _probe_floats(3)
+    with np.errstate(over="ignore"):
+        assert np.array_equal(orc.f32_to_f16_bits_hw(x), x.astype(np.float16).view(np.uint16))
+
+
 def test_f32_to_bf16_round_to_nearest_even():
     x = _probe_floats(1)
     rng = np.random.default_rng(2)

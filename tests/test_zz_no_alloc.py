@@ -36,7 +36,7 @@ def _pair(q, k, v, rope, norm, out_dtype=torch.float32):
     dw = kd_fa.make_desc(q, k, v, None, out_w, 1.0 / D ** 0.5)
     st = kd_fa.run_static(ds, rope, norm)
     assert st == kd_fa.OK, kd_fa.lib().kd_fa_strerror(st)
-    ws = torch.empty(max(kd_fa.workspace_size(dw), 16) // 2, dtype=v.dtype, device=DEV)
+    ws = torch.empty(max(kd_fa.workspace_size(dw), 16), dtype=torch.uint8, device=DEV)
     st = kd_fa.run_desc(dw, rope, None, ws, norm if norm is not None else kd_fa.qk_norm(None, None))
     assert st == kd_fa.OK
     torch.cuda.synchronize()
@@ -91,3 +91,35 @@ def test_static_scratch_c1_shape_and_plain_node():
     assert torch.equal(a, b)
     a, b = _pair(q, k, v, None, None)
     assert torch.equal(a, b)
+
+
+def test_static_scratch_k_over_the_limit_runs_without_it():
+    """A 16-bit K whose transformed copy exceeds the static array (32 heads
+    x 8,193 keys x 256 B = 64 MiB + 8 KiB) runs without a workspace (K
+    transformed in staged groups or on load) and gives the caller-workspace
+    call's bits."""
+    _need_gpu()
+    _announce("static scratch: [128,8193,32,1] bf16 rope, K over the array")
+    L, H = 8193, 32
+    q, k, v = (t.to(DEV) for t in qkv(1, H, L, L, torch.bfloat16, seed=311))
+    table = kd_fa.text_rope_table(L, D)
+    rope = kd_fa.rope_table(torch.from_numpy(table).to(DEV))
+    d = kd_fa.make_desc(q, k, v, None, torch.empty((1, L, H, D), device=DEV), 1.0 / D ** 0.5)
+    assert kd_fa.workspace_size(d) > kd_fa.STATIC_SCRATCH_BYTES
+    a, b = _pair(q, k, v, rope, None)
+    assert torch.equal(a, b)
+    assert torch.isfinite(a).all()
+
+
+def test_static_scratch_f32_k_and_v():
+    """Q, K, V F32 (the projections ops::attention receives), K and V cast to
+    F16 into the static array: the caller-workspace call's bits."""
+    _need_gpu()
+    _announce("static scratch: [128,1280,32,1] all F32, cast F16, rope")
+    T, Hp, Wp = 5, 16, 16
+    L = T * Hp * Wp
+    q, k, v = (t.to(DEV) for t in qkv(1, 32, L, L, torch.float32, seed=312))
+    _, rope = _rope(T, Hp, Wp)
+    a, b = _pair(q, k, v, rope, kd_fa.qk_norm(None, None, 1e-6))
+    assert torch.equal(a, b)
+    assert torch.isfinite(a).all()
