@@ -200,3 +200,44 @@ def test_c3_all_f32_sampled():
     ref = orc.fa_f64(q2, k2, v2, rows=rows)
     m = assert_parity(gather_rows(out, rows, HEADS, L), ref, "C3 all-F32")
     print(f"[C3 all-F32] {m}", flush=True)
+
+
+@pytest.mark.parametrize("cast", [torch.float16, torch.bfloat16])
+def test_masked_cross_attention_from_f32_projections(cast):
+    """The cross-attention of DiTCrossAttention from its projections: Q, K, V
+    F32, the key norm, a padding mask, 256 keys and 2,048 query rows per head
+    (65,536 in all, so the mask summary runs): the workspace holds K, then V,
+    then the summary, and the result is the call on the oracle-rounded
+    operands, bitwise, and within the oracle gate on every row."""
+    _need_gpu()
+    _announce(f"masked cross-attention from F32 projections, cast {cast}")
+    B, H, Lq, Lk = 2, 16, 2048, 256
+    q = randn((B, H, Lq, D), torch.float32, 521)
+    k = randn((B, H, Lk, D), torch.float32, 522) * 1.5
+    v = randn((B, H, Lk, D), torch.float32, 523)
+    from fa_common import padding_mask
+    m = padding_mask(B, Lq, Lk, (200, 37))
+    g = torch.Generator().manual_seed(524)
+    wq = (torch.randn(D, generator=g) * 0.3 + 1.0).float()
+    wk = (torch.randn(D, generator=g) * 0.3 + 1.0).float()
+    norm = kd_fa.qk_norm(wq.to(DEV), wk.to(DEV), EPS)
+    ct = kd_fa.TYPE_BF16 if cast == torch.bfloat16 else kd_fa.TYPE_F16
+    qg, kg, vg, mg = q.to(DEV), k.to(DEV), v.to(DEV), m.to(DEV)
+    out = torch.full((B, Lq, H, D), float("nan"), device=DEV)
+    d = kd_fa.make_desc(qg, kg, vg, mg, out, SCALE, cast_type=ct)
+    n_ws = kd_fa.workspace_size_full(d, None, norm)
+    kb = B * H * Lk * D * 2
+    assert n_ws == 2 * kb + 4 * B * ((Lq + 31) // 32)      # K, V, then one word per batch and 32 rows
+    ws = torch.full((n_ws,), 0xAB, dtype=torch.uint8, device=DEV)
+    assert kd_fa.run_desc(d, None, None, ws, norm) == kd_fa.OK
+    torch.cuda.synchronize()
+    k2 = _round(_norm(k, wk), cast)
+    v2 = _round(v, cast)
+    assert torch.equal(ws[:kb].view(cast).view(k2.shape).cpu(), k2)
+    assert torch.equal(ws[kb:2 * kb].view(cast).view(v2.shape).cpu(), v2)
+    q2 = _round(_norm(q, wq), cast)
+    plain = kd_fa.flash_attn_ext(q2.to(DEV), k2.to(DEV), v2.to(DEV), mask=mg)
+    torch.cuda.synchronize()
+    assert torch.equal(out, plain)
+    rows = np.arange(B * H * Lq)
+    assert_parity(gather_rows(out, rows, H, Lq), orc.fa_f64(q2, k2, v2, mask=m), f"masked cross F32 {cast}")
