@@ -186,7 +186,7 @@ int kd_fa_run(const kd_fa_desc *desc, void *stream);
  * written by a pass over the mask on `stream`, so that the attention skips
  * the fully masked tiles of a block without loading their mask rows; the
  * result is bitwise kd_fa_run's.  The VAE's one-head D = 512 node
- * (src/models/vae.hpp:60-101) at short token counts (fewer than 256 blocks
+ * (src/models/vae.hpp:60-101) at short token counts (fewer than 512 blocks
  * of 32 query rows: the 64x64 latent) splits every row's keys into ranges
  * computed side by side, their partial results kept in the workspace and
  * merged by a second pass; the result then differs from kd_fa_run's only

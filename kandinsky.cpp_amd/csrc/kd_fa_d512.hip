@@ -28,9 +28,13 @@ namespace kdfa {
 //           the weights P (rounded to the operand type), the rescale factor
 //           and, at the end, the row sum to LDS for all waves;
 //   O_w^T = alpha * O_w^T + V_w^T P^T (8 MFMA per row block), V_w staged by
-//           DMA in the wave's own LDS region (double-buffered, no barrier:
-//           only that wave reads it) and read transposed with
-//           ds_read_b64_tr_b16, each fragment once for all R blocks.
+//           DMA in the wave's own LDS region (NB buffers, no barrier: only
+//           that wave reads it) and read transposed with ds_read_b64_tr_b16,
+//           each fragment once for all R blocks.
+// NB = 2 (R = 2): V(t+1) staged during tile t, one workgroup per CU.  NB = 1
+// (R = 1, 54 KB of LDS, 228 registers): two workgroups per CU, so that one
+// hides the other's barrier and LDS round trips; V(t+1) is staged once
+// PV(t) has read V(t), and K is loaded two tiles ahead instead.
 // Two barriers per tile.  Keys past Lk (last tile) load clamped rows and get
 // weight 0.  Every K and V byte a workgroup streams serves 32R query rows:
 // with R = 2 the key stream of the long latents (16,384 keys, all of them
@@ -48,8 +52,9 @@ constexpr int kD5VTile = kD5Keys * 256;        // one wave's V tile: 32 keys x 1
 
 static_assert(kD5 == 4 * 128, "one 128-column slice per wave");
 
-template <typename T, int R>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void fa_fwd_d512(Args a) {
+template <typename T, int R, int NB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB == 1 ? 2 : 1, NB == 1 ? 2 : 1)))
+void fa_fwd_d512(Args a) {
     typedef Elem<T> E;
     typedef typename E::vec8 vec8;
     constexpr int kRows = 32 * R;                  // query rows per workgroup
@@ -59,7 +64,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     __shared__ __attribute__((aligned(16))) uint16_t sP[kRows][kD5PStride];
     __shared__ float sAlpha[kRows];
     __shared__ float sL[kRows];
-    __shared__ __attribute__((aligned(1024))) char sV[4][2][kD5VTile];
+    __shared__ __attribute__((aligned(1024))) char sV[4][NB][kD5VTile];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -145,12 +150,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // compiler's vmcnt bookkeeping) before the K loads, so that the
     // compiler's own waits for K stay exact (loads complete in order) and
     // V(t) has landed once at most the 16 newer loads are in flight
-    vec8 kf[8];
+    // NB = 1 (one V buffer per wave, two workgroups per CU): K fragments
+    // two tiles ahead in two register sets, V(t+1) staged once PV(t) has
+    // read V(t); VMEM order K(t+2) .. V(t+1), so the compiler's wait for K
+    // never waits for the V DMA issued after it
+    vec8 kf[NB == 1 ? 2 : 1][8];
     if (n_tiles > t_begin) {
-        issue_v(t_begin, t_begin & 1);
-        load_k(t_begin, kf);
+        if constexpr (NB == 2) {
+            issue_v(t_begin, t_begin & 1);
+            load_k(t_begin, kf[0]);
+        } else {
+            load_k(t_begin, kf[0]);
+            if (t_begin + 1 < n_tiles) load_k(t_begin + 1, kf[1]);
+            issue_v(t_begin, 0);
+        }
     }
-    for (int t = t_begin; t < n_tiles; ++t) {
+    auto tile = [&](int t, auto kb_c) __attribute__((always_inline)) {
+        constexpr int kb = decltype(kb_c)::value ? 1 : 0;
         // the Q fragments (read by the matrix unit only) live in AGPRs, so
         // that O, S and the K fragments have the VGPRs to themselves
 #pragma unroll
@@ -163,11 +179,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         for (int rb = 0; rb < R; ++rb) {
             s[rb] = (f32x16){};
 #pragma unroll
-            for (int ks = 0; ks < 8; ++ks) s[rb] = E::mfma(kf[ks], qf[rb][ks], s[rb]);
+            for (int ks = 0; ks < 8; ++ks) s[rb] = E::mfma(kf[kb][ks], qf[rb][ks], s[rb]);
         }
-        if (t + 1 < n_tiles) {
-            issue_v(t + 1, (t + 1) & 1);
-            load_k(t + 1, kf);
+        if constexpr (NB == 2) {
+            if (t + 1 < n_tiles) {
+                issue_v(t + 1, (t + 1) & 1);
+                load_k(t + 1, kf[0]);
+            }
+        } else {
+            if (t + 2 < n_tiles) load_k(t + 2, kf[kb]);
         }
         // element i of lane l: key 8*(i/4) + 4*hi + i%4, query l32
 #pragma unroll
@@ -229,11 +249,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                     for (int i = 0; i < 16; ++i) o[rb][dblk][i] *= al;
             }
         }
-        if (t + 1 < n_tiles)
-            asm volatile("s_waitcnt vmcnt(16)" ::: "memory");   // V(t) landed; V(t+1), K(t+1) may fly
-        else
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        const lds_t *vs_ = LDS_PTR(char, sV[wave][t & 1]);
+        if constexpr (NB == 2) {
+            if (t + 1 < n_tiles)
+                asm volatile("s_waitcnt vmcnt(16)" ::: "memory");   // V(t) landed; V(t+1), K(t+1) may fly
+            else
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        } else {
+            if (t + 2 < n_tiles)
+                asm volatile("s_waitcnt vmcnt(8)" ::: "memory");    // V(t) landed; K(t+2) may fly
+            else
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        const lds_t *vs_ = LDS_PTR(char, sV[wave][NB == 2 ? (t & 1) : 0]);
 #pragma unroll
         for (int kst = 0; kst < kD5Keys / 16; ++kst) {
             vec8 pb[R];
@@ -249,6 +276,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 for (int rb = 0; rb < R; ++rb) o[rb][dblk] = E::mfma(va, pb[rb], o[rb][dblk]);
             }
         }
+        if constexpr (NB == 1) {
+            if (t + 1 < n_tiles) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's V(t) reads are done
+                issue_v(t + 1, 0);
+            }
+        }
+    };
+    for (int t = t_begin; t < n_tiles; t += NB == 1 ? 2 : 1) {
+        tile(t, BC<false>());
+        if constexpr (NB == 1)
+            if (t + 1 < n_tiles) tile(t + 1, BC<true>());
     }
     if (a.n_split > 1) {
         // this range's unnormalised O (times exactly 1), running max and row
@@ -316,10 +354,10 @@ __global__ __launch_bounds__(256) void d512_combine(Args a) {
     }
 }
 
-template <typename T, int R>
+template <typename T, int R, int NB>
 static hipError_t launch_d512_t(const Args &a, hipStream_t s) {
     const int64_t grid = (int64_t)a.n_blocks * (a.n_split > 1 ? a.n_split : 1);
-    hipLaunchKernelGGL((fa_fwd_d512<T, R>), dim3((unsigned)grid), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((fa_fwd_d512<T, R, NB>), dim3((unsigned)grid), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -329,10 +367,14 @@ hipError_t launch_d512_combine(const Args &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// 64-row workgroups (R = 2): one per CU, V double-buffered; 32-row ones
+// (R = 1): two per CU, one V buffer per wave (4,096 tokens with the key
+// split 0.115 -> 0.106 ms, without 0.188 -> 0.181; 1,024 tokens 0.053 ->
+// 0.050; the same bits)
 hipError_t launch_d512(const Args &a, int kv_type, int rows, hipStream_t stream) {
     if (rows == 64)
-        return kv_type == KD_FA_TYPE_BF16 ? launch_d512_t<__bf16, 2>(a, stream) : launch_d512_t<_Float16, 2>(a, stream);
-    return kv_type == KD_FA_TYPE_BF16 ? launch_d512_t<__bf16, 1>(a, stream) : launch_d512_t<_Float16, 1>(a, stream);
+        return kv_type == KD_FA_TYPE_BF16 ? launch_d512_t<__bf16, 2, 2>(a, stream) : launch_d512_t<_Float16, 2, 2>(a, stream);
+    return kv_type == KD_FA_TYPE_BF16 ? launch_d512_t<__bf16, 1, 1>(a, stream) : launch_d512_t<_Float16, 1, 1>(a, stream);
 }
 
 }  // namespace kdfa

@@ -17,6 +17,9 @@
 
 namespace kdfa {
 
+// a compile-time flag passed to generic lambdas (BC<true>(), BC<false>())
+template <bool B> struct BC { static constexpr bool value = B; };
+
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));

@@ -169,8 +169,8 @@ int device_ok() {
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
 // Key split of the D = 512 kernel through the workspace (kd_fa_run_ws):
-// when its 32-row workgroups would leave CUs idle (fewer than 256: the VAE's
-// 64x64 latent, 4,096 tokens, gives 128) and there are at least four key
+// when its 32-row workgroups (two per CU) would leave CUs idle (fewer than
+// 512: the VAE's 64x64 latent, 4,096 tokens, gives 128) and there are at least four key
 // tiles (at two, 9.1 against 11.5 us), each row block's keys are cut into
 // S ranges of whole 32-key tiles (S <= 8, one workgroup per range), whose
 // unnormalised partial results a second pass merges.  `bytes`: the partial
@@ -180,13 +180,14 @@ struct D512Split {
     int keys = 0;
     size_t bytes = 0;
 };
+constexpr int64_t kD512Slots = 512;   // 32-row workgroups resident at once: two per CU
 D512Split d512_split(int64_t Lq, int64_t Lk, int64_t H, int64_t B, int route) {
     D512Split r;
     const int64_t nb32 = (Lq + 31) / 32 * H * B;
-    if ((route & KD_FA_ROUTE_NO_SPLIT) || nb32 >= 256 || nb32 == 0) return r;
+    if ((route & KD_FA_ROUTE_NO_SPLIT) || nb32 >= kD512Slots || nb32 == 0) return r;
     const int64_t tiles = (Lk + 31) / 32;
     if (tiles < 4) return r;   // the merge's launch outweighs splitting one to three tiles
-    int64_t S = std::min<int64_t>(std::min<int64_t>(8, 256 / nb32), tiles);
+    int64_t S = std::min<int64_t>(std::min<int64_t>(8, kD512Slots / nb32), tiles);
     if (S < 2) return r;
     const int64_t per = (tiles + S - 1) / S;   // tiles per range
     S = (tiles + per - 1) / per;

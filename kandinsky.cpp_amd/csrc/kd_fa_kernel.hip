@@ -35,8 +35,6 @@ namespace kdfa {
 constexpr int kBN = 64;                             // keys per tile
 constexpr int kTileBytes = kBN * kD * 2;            // one K or V tile
 
-template <bool B> struct BC { static constexpr bool value = B; };
-
 // Instruction order of one S^T product for the scheduler: PRE pairs of K
 // fragment reads ahead, then per k-step two MFMAs and the next pair of reads.
 // (sched_group_barrier masks: 0x008 MFMA, 0x100 DS read.)

@@ -268,15 +268,16 @@ def test_full_workspace_size_holds_k_then_mask_summary():
 
 def test_vae_node_workspace_is_the_key_split():
     """The D = 512 node takes a workspace for its key split when fewer than
-    256 blocks of 32 query rows run and there are at least four key tiles:
-    2 ranges at 4,096 tokens, 8 at 1,024, none at 16,384; 2,056 bytes per
-    query row and range."""
+    512 blocks of 32 query rows run (two workgroups per CU) and there are at
+    least four key tiles: 4 ranges at 4,096 tokens, 8 at 1,024, 2 at 8,192,
+    none at 16,384; 2,056 bytes per query row and range."""
     def size(Lq, Lk, H=1, B=1):
         q = torch.zeros((B, H, Lq, 512))
         k = torch.zeros((B, H, Lk, 512), dtype=torch.float16)
         dst = torch.zeros((B, Lq, H, 512))
         return kd_fa.workspace_size_full(kd_fa.make_desc(q, k, k, None, dst, 0.04))
-    assert size(4096, 4096) == 2 * 4096 * 2056
+    assert size(4096, 4096) == 4 * 4096 * 2056
+    assert size(8192, 8192) == 2 * 8192 * 2056
     assert size(1024, 1024) == 8 * 1024 * 2056
     assert size(300, 1000) == 8 * 300 * 2056          # 32 tiles / 8 ranges of 4
     assert size(64, 130) == 5 * 64 * 2056             # five tiles, five ranges

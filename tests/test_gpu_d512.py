@@ -148,13 +148,14 @@ def test_d512_vae_128x128_sampled():
 
 def _split_ranges(Lq, Lk, H, B):
     """(ranges, keys per range) of the key split kd_fa_run_ws takes for a
-    D = 512 node: fewer than 256 blocks of 32 query rows and at least four
-    key tiles, at most 8 ranges of whole 32-key tiles, at least two."""
+    D = 512 node: fewer than 512 blocks of 32 query rows (two workgroups per
+    CU) and at least four key tiles, at most 8 ranges of whole 32-key tiles,
+    at least two."""
     nb = (Lq + 31) // 32 * H * B
     tiles = (Lk + 31) // 32
-    if nb >= 256 or tiles < 4:
+    if nb >= 512 or tiles < 4:
         return 1, 0
-    S = min(8, 256 // nb, tiles)
+    S = min(8, 512 // nb, tiles)
     if S < 2:
         return 1, 0
     per = (tiles + S - 1) // S
@@ -164,7 +165,8 @@ def _split_ranges(Lq, Lk, H, B):
 
 SPLIT_CASES = [
     # B, H, Hkv, Bk, Lq, Lk, K/V type, dst type
-    (1, 1, 1, 1, 4096, 4096, torch.float16, torch.float32),    # 64x64 latent: two key ranges
+    (1, 1, 1, 1, 4096, 4096, torch.float16, torch.float32),    # 64x64 latent: four key ranges
+    (1, 1, 1, 1, 8192, 2048, torch.bfloat16, torch.float32),   # 256 blocks: two ranges
     (1, 1, 1, 1, 1024, 1024, torch.float16, torch.float32),    # 32x32 latent: eight ranges
     (1, 1, 1, 1, 300, 1000, torch.bfloat16, torch.float32),    # ragged last tile and range
     (2, 2, 1, 1, 100, 200, torch.float16, torch.bfloat16),     # GQA and batch broadcast, 16-bit dst
