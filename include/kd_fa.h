@@ -368,15 +368,18 @@ int kd_fa_dit_run_static(const kd_fa_desc *desc, const kd_fa_rope *rope, const k
  */
 enum {
     KD_FA_ROUTE_DEFAULT = 0,
-    KD_FA_ROUTE_NO_W64  = 1,   /* unmasked calls: the 32-row kernel, not the 64-row one   */
+    KD_FA_ROUTE_NO_W64  = 1,   /* unmasked calls: the 32-row kernel, not the 64-row or
+                                  the persistent long-prompt one                       */
     KD_FA_ROUTE_NO_XRES = 2,   /* short key sets: the 32-row kernel, not the LDS-resident */
     KD_FA_ROUTE_D512_R1 = 4,   /* D = 512: one 32-row block per workgroup                 */
     KD_FA_ROUTE_NO_SPLIT = 8,  /* D = 512, short query sets: no key split (one pass)     */
     KD_FA_ROUTE_W64_SHORT = 16, /* unmasked key sets <= 896 too: the 64-row kernel       */
     KD_FA_ROUTE_STAGED = 32,    /* K transformed without a workspace: staged whenever the
                                    shape allows, also where one on-load launch is cheaper */
-    KD_FA_ROUTE_SUMMARY = 64    /* mask summary for every masked short-key node with the
+    KD_FA_ROUTE_SUMMARY = 64,   /* mask summary for every masked short-key node with the
                                    workspace, also below 65,536 query rows             */
+    KD_FA_ROUTE_NO_XLONG = 128  /* unmasked key sets of 257-1,024 keys: the 32-row
+                                   kernel, not the persistent long-prompt one          */
 };
 int kd_fa_set_routing(int flags);
 

@@ -19,6 +19,8 @@ namespace kdfa {
 
 // a compile-time flag passed to generic lambdas (BC<true>(), BC<false>())
 template <bool B> struct BC { static constexpr bool value = B; };
+// a compile-time integer passed the same way
+template <int I> struct IC { static constexpr int value = I; };
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));

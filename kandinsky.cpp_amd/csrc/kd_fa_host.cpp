@@ -251,12 +251,14 @@ static bool w64_tail_ok(const kdfa::Args &a) { return a.Lk % 64 == 0 || a.scale_
 
 // The 64-rows-per-wave kernel takes the unmasked calls whose K streams from
 // memory as stored (no transform on load) and that have more than
-// kShortKeys keys; its buffer-resource offsets are 32-bit.  (With one
+// kShortKeys keys and that the long-prompt kernel does not take (use_xlong
+// is asked first); its buffer-resource offsets are 32-bit.  (With one
 // workgroup per CU, all CUs load Q, run the few key steps of a short key set
 // and store O in step, while the 32-row kernel's 4-wave workgroups, two per
 // CU, overlap one's memory phases with the other's key loop: cross-attention
 // with Q F32 [128, 31744, 32, 2] and 320 keys 0.62 against 0.72 ms, 512
-// keys 0.78 against 0.85, 896 keys 1.14 against 1.15, 1,024 keys even.)
+// keys 0.78 against 0.85, 896 keys 1.14 against 1.15, 1,024 keys even --
+// the range where the persistent long-prompt kernel now runs when it can.)
 // For comparisons, KD_FA_ROUTE_NO_W64 routes every call to the 32-row
 // kernel and KD_FA_ROUTE_W64_SHORT the short key sets too to this one.
 static bool use_w64(const kdfa::Args &a, bool k_on_load, int route) {
@@ -277,6 +279,21 @@ static bool use_xres(const kdfa::Args &a, int op, const kd_fa_desc *d, bool k_on
     if (a.q_type != KD_FA_TYPE_F32 && a.q_type != op) return false;
     if (a.m && (!a.mask_vec || d->mask.ne[0] < ((int64_t)a.Lk + 7) / 8 * 8)) return false;
     return true;
+}
+
+// Unmasked key sets just past the LDS-resident kernel's (the text
+// cross-attention of a long prompt) go to the persistent kernel that streams
+// K and V with the next query tile's Q loaded during the key loop, when K is
+// read as stored, Q is neither rotated nor normalised and is stored as F32
+// or in K's type, and a unit's Q rows lie within 32-bit offsets of its first
+// row.  KD_FA_ROUTE_NO_XLONG and KD_FA_ROUTE_NO_W64 route them to the 32-row
+// kernel, KD_FA_ROUTE_W64_SHORT to the 64-row one (for comparisons).
+static bool use_xlong(const kdfa::Args &a, int op, bool k_on_load, int route) {
+    if (route & (KD_FA_ROUTE_NO_XLONG | KD_FA_ROUTE_NO_W64 | KD_FA_ROUTE_W64_SHORT)) return false;
+    if (a.m || k_on_load || a.rope_mode != KD_FA_ROPE_NONE || a.qn_w) return false;
+    if (a.Lk <= kdfa::kXresMaxKeys || a.Lk > kdfa::kXlongMaxKeys) return false;
+    if (a.q_type != KD_FA_TYPE_F32 && a.q_type != op) return false;
+    return (int64_t)(kdfa::kXlongRows - 1) * a.q_nb1 + 512 < ((int64_t)1 << 32);
 }
 
 // Query ranges per (b, h) for fa_fwd_xres: about one workgroup per CU
@@ -640,6 +657,10 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
             a.m_live_nqb = (int32_t)((Lq + 31) / 32);
         }
         e = kdfa::launch_xres(a, T, hs);
+    } else if (use_xlong(a, T, k_rope, route)) {
+        a.n_qt = (int32_t)((Lq + kdfa::kXlongRows - 1) / kdfa::kXlongRows);
+        a.n_blocks = (int32_t)(a.n_qt * H * B);
+        e = kdfa::launch_xlong(a, T, hs);
     } else if (use_w64(a, k_rope, route)) {
         a.n_qt = (int32_t)((Lq + kdfa::kW64Rows - 1) / kdfa::kW64Rows);
         a.n_blocks = (int32_t)(a.n_qt * H * B);

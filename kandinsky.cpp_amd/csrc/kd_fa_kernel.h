@@ -97,6 +97,18 @@ hipError_t launch_w64(const Args &a, int kv_type, hipStream_t stream);
 constexpr int kXresMaxKeys = 256;
 hipError_t launch_xres(const Args &a, int kv_type, hipStream_t stream);
 
+// Enqueue the persistent long-prompt kernel (no mask, K as stored, Q F32 or
+// in K's type and neither rotated nor normalised, kXresMaxKeys < Lk <=
+// kXlongMaxKeys, Q row offsets of a unit within 32 bits): units of
+// kXlongRows query rows of one (b, h), a.n_qt per (b, h) and a.n_blocks in
+// all, walked by at most one workgroup per CU.  (Above 1,024 keys the
+// 64-row kernel's faster key loop outweighs the overlapped memory phases:
+// Q F32 [128, 31744, 32, 2] with F16 K/V, 1,024 keys 1.20 against 1.22 ms,
+// 1,536 keys 1.66 against 1.61.)
+constexpr int kXlongRows = 256;
+constexpr int kXlongMaxKeys = 1024;
+hipError_t launch_xlong(const Args &a, int kv_type, hipStream_t stream);
+
 // Enqueue the mask summary fa_fwd_xres reads through a.m_live: one 32-bit
 // word per (mask batch, mask head, 32-row query block) of the call's mask
 // (rows past Lq clamped to Lq - 1, keys below Lk, Lk <= kXresMaxKeys, rows

@@ -1316,6 +1316,517 @@ void fa_fwd_xres(Args a) {
 }
 
 // ---------------------------------------------------------------------------
+// fa_fwd_xlong: unmasked key sets of kXresMaxKeys + 1 .. kXlongMaxKeys keys,
+// K read as stored, Q neither rotated nor normalised -- the text
+// cross-attention of a long prompt (src/models/crossdit.hpp:198 calls
+// ops::attention without a mask; the tokenizer keeps up to 512 prompt
+// tokens, src/models/qwen_tokenizer.hpp:128,183-186).  K and V of 512 keys
+// (256 KiB in 16 bits) do not fit the LDS, so they stream through it tile by
+// tile, in fa_fwd_d128's pipelined unmasked loop (the scores of tile t+1
+// computed between the softmax instructions of tile t; K two tiles and V one
+// tile ahead by DMA).  What this kernel adds is that a workgroup's memory
+// phases overlap its key loop instead of running in sequence with it:
+//
+// * Persistent workgroups.  One 8-wave workgroup per CU walks units of 256
+//   query rows of one (b, h): XCD x (workgroups are dealt to the XCDs
+//   round-robin) owns a contiguous range of units and its workgroup j takes
+//   units j, j + w, j + 2w, ... of it (w workgroups per XCD), so that an
+//   XCD's workgroups run neighbouring query tiles of one head together and
+//   share its K and V in the L2.
+// * Q by DMA during the key loop.  In the first kPieces steps of a unit,
+//   each wave brings 128 bytes of each of its 32 rows of the next unit into
+//   its raw area (one piece per step) and, a step later, rounds them to the
+//   operand type into its fragment area, from which the next unit loads its
+//   Q fragments with eight LDS reads.
+// * The next unit's first tiles ahead of the O stores.  The last step of a
+//   unit fetches the next unit's K(0) and K(1) (its K buffers are free by
+//   then), V(0) follows once the step's products are done, and only then
+//   are the unit's O stores issued: the wait before the next unit's first
+//   step counts the stores issued after V(0) and does not wait for them
+//   (loads and stores complete in issue order).
+//
+// Each unit starts like fa_fwd_d128's loop (the exact max of its first
+// tile's scores, then the lazy running max), and per row the arithmetic is
+// that loop's, so the two kernels give bitwise equal results.
+//
+// LDS (one object, the tiles first so that every fragment address is a lane
+// offset plus an immediate below 64 KiB): K and V tiles 2 x 2 x 16 KiB, then
+// per wave 8 KiB of Q fragments (lane l's fragment of k-step ks at
+// ks * 1024 + 16 l) and 4 KiB of raw Q rows (row r of the wave at 128 r, its
+// 16-byte chunk c at c ^ (r & 7)), which also stage the O rows of the
+// epilogue: 160 KiB.
+// ---------------------------------------------------------------------------
+constexpr int kLWaves = 8;
+constexpr int kLRows = 32 * kLWaves;   // query rows per unit
+constexpr int kLFrag = 8192;           // per wave: 8 k-steps x 64 lanes x 16 bytes
+constexpr int kLRaw = 4096;            // per wave: 128 bytes of each of its 32 rows
+static_assert(kLRows == kXlongRows, "unit size");
+
+template <typename T, bool Q32>
+__global__ __launch_bounds__(64 * kLWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void fa_fwd_xlong(Args a) {
+    constexpr int kThreads = 64 * kLWaves;
+    constexpr int kRounds = kTileBytes / (kThreads * 16);
+    static_assert(kRounds * kThreads * 16 == kTileBytes, "tile shape");
+    constexpr int kPieces = Q32 ? 4 : 2;   // 128-byte pieces of a Q row
+    constexpr int kKPre = kKPreDma;
+    typedef Elem<T> E;
+    typedef typename E::vec8 vec8;
+    __shared__ __attribute__((aligned(1024))) char lds[4 * kTileBytes + kLWaves * (kLFrag + kLRaw)];
+    lds_t *const sK0 = LDS_PTR(char, lds), *const sK1 = sK0 + kTileBytes;
+    lds_t *const sV0 = sK0 + 2 * kTileBytes, *const sV1 = sK0 + 3 * kTileBytes;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31;
+    const int hi = lane >> 5;
+    lds_t *const sQf = sK0 + 4 * kTileBytes + wave * (kLFrag + kLRaw);
+    lds_t *const sRaw = sQf + kLFrag;
+
+    // this workgroup's units: j, j + wpx, ... within its XCD's range
+    const int n_units = a.n_blocks;
+    const int wpx = (int)(gridDim.x >> 3);
+    const int per = (n_units + 7) >> 3;
+    const int xcd = (int)(blockIdx.x & 7);
+    const int u_end = min((xcd + 1) * per, n_units);
+    int u = xcd * per + (int)(blockIdx.x >> 3);
+    if (u >= u_end) return;   // before any barrier
+
+    const int Lk = a.Lk, Lq = a.Lq;
+    const int n_tiles = (Lk + kBN - 1) / kBN;   // >= 5
+    const float c2 = __builtin_fabsf(a.scale_log2);
+
+    // A unit's values come from the kernel arguments read again through a
+    // pointer made opaque at each use, so that the arguments the key loop
+    // does not need are not held in scalar registers across it.
+    typedef const __attribute__((address_space(4))) Args *args_ptr;
+    auto kargs = []() __attribute__((always_inline)) {
+        args_ptr ap = (args_ptr)__builtin_amdgcn_kernarg_segment_ptr();
+        asm volatile("" : "+s"(ap));
+        return ap;
+    };
+    struct Unit {
+        const char *k, *v, *q;   // K, V of its (b, h); Q from its first row
+        char *o;                 // O from its first row
+        int row0;
+    };
+    auto unit_at = [&](int uu) __attribute__((always_inline)) {
+        const args_ptr ap = kargs();
+        Unit r;
+        const int qt = uu % ap->n_qt;
+        const int bh = uu / ap->n_qt;
+        const int h = bh % ap->H;
+        const int b = bh / ap->H;
+        r.row0 = qt * kLRows;
+        r.o = ap->o + (int64_t)b * ap->o_nb3 + (int64_t)h * ap->o_nb1 + (int64_t)r.row0 * ap->o_nb2;
+        r.k = ap->k + (int64_t)(h / ap->rk2) * ap->k_nb2 + (int64_t)(b / ap->rk3) * ap->k_nb3;
+        r.v = ap->v + (int64_t)(h / ap->rv2) * ap->v_nb2 + (int64_t)(b / ap->rv3) * ap->v_nb3;
+        r.q = ap->q + (int64_t)h * ap->q_nb2 + (int64_t)b * ap->q_nb3 + (int64_t)r.row0 * ap->q_nb1;
+        return r;
+    };
+    // a fresh opaque copy of the lane index at each use outside the key
+    // products: what is derived from it (the partial tile's key tests and
+    // clamped DMA offsets, the Q pieces' and O rows' addresses) is computed
+    // at its use instead of being held across the loops
+    auto fresh_lane = [&]() __attribute__((always_inline)) {
+        int x = lane;
+        asm volatile("" : "+v"(x));
+        return x;
+    };
+
+    // ---- K/V tile DMA (fa_fwd_d128's lanes, rows and swizzles) ---------------
+    const uint32_t v_dma0 = (uint32_t)(4 * wave + (lane >> 4)) * (uint32_t)a.v_nb1 +
+                            (((lane & 15) ^ v_swz(4 * wave + (lane >> 4))) << 4);
+    const uint32_t k_dma0 = (uint32_t)k_row_of(4 * wave + (lane >> 4)) * (uint32_t)a.k_nb1 +
+                            (((lane & 15) ^ ((4 * wave + (lane >> 4)) & 15)) << 4);
+    auto issue_v = [&](const char *vb, int t, lds_t *dV) __attribute__((always_inline)) {
+        const char *vt = vb + (int64_t)t * kBN * a.v_nb1;
+        if ((t + 1) * kBN <= Lk) {
+#pragma unroll
+            for (int j = 0; j < kRounds; ++j)
+                dma16(vt + (int64_t)j * 4 * kLWaves * a.v_nb1, v_dma0, dV + (wave + kLWaves * j) * 1024);
+        } else {
+            const int ln = fresh_lane();
+#pragma unroll
+            for (int j = 0; j < kRounds; ++j) {
+                const int r = 4 * (wave + kLWaves * j) + (ln >> 4);
+                const int vr = t * kBN + r < Lk ? r : Lk - 1 - t * kBN;
+                dma16(vt, (uint32_t)vr * (uint32_t)a.v_nb1 + (((ln & 15) ^ v_swz(r)) << 4),
+                      dV + (wave + kLWaves * j) * 1024);
+            }
+        }
+    };
+    auto issue_k = [&](const char *kb, int t, lds_t *dK) __attribute__((always_inline)) {
+        const char *kt = kb + (int64_t)t * kBN * a.k_nb1;
+        if ((t + 1) * kBN <= Lk) {
+#pragma unroll
+            for (int j = 0; j < kRounds; ++j)
+                dma16(kt + (int64_t)j * 4 * kLWaves * a.k_nb1, k_dma0, dK + (wave + kLWaves * j) * 1024);
+        } else {
+            const int ln = fresh_lane();
+#pragma unroll
+            for (int j = 0; j < kRounds; ++j) {
+                const int r = 4 * (wave + kLWaves * j) + (ln >> 4);
+                const int kr = t * kBN + k_row_of(r) < Lk ? k_row_of(r) : Lk - 1 - t * kBN;
+                dma16(kt, (uint32_t)kr * (uint32_t)a.k_nb1 + (((ln & 15) ^ (r & 15)) << 4),
+                      dK + (wave + kLWaves * j) * 1024);
+            }
+        }
+    };
+
+    // ---- the next unit's Q -----------------------------------------------------
+    // Piece p of a row is its bytes 128 p .. +127 (F32: k-steps 2p, 2p+1;
+    // 16-bit: k-steps 4p .. 4p+3).  DMA instruction jj of a piece fills rows
+    // 8 jj .. +7 of the raw area: lane l fills slot l % 8 of row 8 jj + l / 8
+    // with the chunk that belongs there.  Rows past Lq read row Lq - 1.
+    auto issue_piece = [&](const Unit &un, int p) __attribute__((always_inline)) {
+        const int ln = fresh_lane();
+        const int pr = ln >> 3;
+        const uint32_t pc16 = (uint32_t)(((ln & 7) ^ (pr & 7)) << 4);
+        const char *qb = un.q + p * 128;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int r = un.row0 + wave * 32 + 8 * jj + pr;
+            const int rc = (r < Lq ? r : Lq - 1) - un.row0;
+            dma16(qb, (uint32_t)rc * (uint32_t)a.q_nb1 + pc16, sRaw + jj * 1024);
+        }
+    };
+    // piece p of this lane's row -> its fragments in the fragment area, with
+    // load_q_frags' rounding and sign (scale < 0 negates Q)
+    auto convert_piece = [&](int p) __attribute__((always_inline)) {
+        const int ln = fresh_lane();
+        const int r32 = ln & 31, h2 = ln >> 5;
+        const lds_t *rp = sRaw + r32 * 128;
+        const int sw = r32 & 7;
+        const uint32_t ng = a.scale_log2 < 0.0f ? 0x80008000u : 0u;
+        if constexpr (Q32) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const f32x4 x0 = *reinterpret_cast<const __attribute__((address_space(3))) f32x4 *>(
+                    rp + (((4 * e + 2 * h2) ^ sw) << 4));
+                const f32x4 x1 = *reinterpret_cast<const __attribute__((address_space(3))) f32x4 *>(
+                    rp + (((4 * e + 2 * h2 + 1) ^ sw) << 4));
+                const u32x4 w = {E::pack2(x0.x, x0.y) ^ ng, E::pack2(x0.z, x0.w) ^ ng, E::pack2(x1.x, x1.y) ^ ng,
+                                 E::pack2(x1.z, x1.w) ^ ng};
+                *reinterpret_cast<__attribute__((address_space(3))) u32x4 *>(sQf + (2 * p + e) * 1024 + ln * 16) = w;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const u32x4 r = *reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(
+                    rp + (((2 * e + h2) ^ sw) << 4));
+                u32x4 w;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) w[j] = E::pack2(E::lo(r[j]), E::hi(r[j])) ^ ng;
+                *reinterpret_cast<__attribute__((address_space(3))) u32x4 *>(sQf + (4 * p + e) * 1024 + ln * 16) = w;
+            }
+        }
+    };
+
+    // ---- per-row state and fa_fwd_d128's arithmetic ------------------------------
+    vec8 qf[8];
+    f32x16 o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = (f32x16){};
+    float m_run = -INFINITY;
+    float l_half = 0.0f;
+
+    uint32_t k_rd[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) k_rd[ks] = l32 * 256 + (((2 * ks + hi) ^ (lane & 15)) << 4);
+    const int v_sub = (lane & 15) >> 2;
+    const int v_c_lo = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+    uint32_t v_rd[4];
+#pragma unroll
+    for (int dblk = 0; dblk < 4; ++dblk)
+        v_rd[dblk] = 2048 * hi + 256 * v_sub + (((4 * dblk + v_c_lo) ^ v_swz(v_sub)) << 4) + 8 * (lane & 1);
+
+    auto qk = [&](const lds_t *ks_, f32x16 &s0, f32x16 &s1) __attribute__((always_inline)) {
+        s0 = (f32x16){};
+        s1 = (f32x16){};
+        vec8 ka[8][2];
+#pragma unroll
+        for (int ks = 0; ks < kKPre; ++ks) {
+            ka[ks][0] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks]);
+            ka[ks][1] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks] + 32 * 256);
+        }
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            if (ks + kKPre < 8) {
+                ka[ks + kKPre][0] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks + kKPre]);
+                ka[ks + kKPre][1] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(ks_ + k_rd[ks + kKPre] + 32 * 256);
+            }
+            s0 = E::mfma(ka[ks][0], qf[ks], s0);
+            s1 = E::mfma(ka[ks][1], qf[ks], s1);
+        }
+        sched_qk<kKPre>();
+    };
+    auto move_max = [&](float mx, bool up) __attribute__((always_inline)) {
+        if (__builtin_amdgcn_ballot_w64(up) != 0) {
+            const float m_new = up ? __builtin_fmaxf(m_run, mx) : m_run;
+            const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            l_half *= alpha;
+#pragma unroll
+            for (int dblk = 0; dblk < 4; ++dblk)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[dblk][i] *= alpha;
+        }
+    };
+    auto pack_sum = [&](const float *p, vec8 pb[4]) -> float {
+        float part[4];
+#pragma unroll
+        for (int kst = 0; kst < 4; ++kst) {
+            u32x4 w;
+            for (int j = 0; j < 4; ++j) w[j] = E::pack2(p[8 * kst + 2 * j], p[8 * kst + 2 * j + 1]);
+            part[kst] = p[8 * kst] + p[8 * kst + 1];
+            for (int i = 2; i < 8; ++i) part[kst] += p[8 * kst + i];
+            pb[kst] = __builtin_bit_cast(vec8, w);
+        }
+        return (part[0] + part[1]) + (part[2] + part[3]);
+    };
+    auto pv = [&](const lds_t *vs_, const vec8 pb[4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int kst = 0; kst < 4; ++kst) {
+#pragma unroll
+            for (int dblk = 0; dblk < 4; ++dblk) {
+                const lds_t *vp = vs_ + v_rd[dblk] + 4096 * kst;
+                const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(vp));
+                const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(vp + 1024));
+                const vec8 va = __builtin_bit_cast(vec8, __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+                o[dblk] = E::mfma(va, pb[kst], o[dblk]);
+            }
+        }
+    };
+
+    // ---- O of a unit: fa_fwd_xres's whole-line stores through LDS ----------------
+    // (the wave's raw area, free once the next unit's last piece is
+    // converted).  F32: 16 store instructions per wave, 16-bit: 8, each
+    // issued unless all of its 8 rows are past Lq.
+    auto flush_unit = [&](const Unit &un) __attribute__((always_inline)) {
+        const int ln = fresh_lane();
+        const int r32 = ln & 31, h2 = ln >> 5;
+        const float l_run = pair_sum(l_half);
+        const float inv = l_run == 0.0f ? 0.0f : 1.0f / l_run;
+        const int rr = ln >> 3;
+        const int rc = ln & 7;
+        const lds_t *const fbase = sRaw + rr * 128 + ((rc ^ rr) << 4);
+        const args_ptr ap = kargs();
+        const int64_t o_nb2 = ap->o_nb2;
+        // row row0 + 32 wave + 8 j + rr at obase + 8 j * o_nb2
+        char *const obase = un.o + (int64_t)(wave * 32 + rr) * o_nb2 + rc * 16;
+        const int rowb = un.row0 + wave * 32 + rr;
+        auto flush = [&](int col_byte) __attribute__((always_inline)) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const u32x4 w = *reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(fbase + j * 1024);
+                if (rowb + 8 * j < Lq)
+                    __builtin_nontemporal_store(w, reinterpret_cast<u32x4 *>(obase + (int64_t)(8 * j) * o_nb2 + col_byte));
+            }
+        };
+        if (ap->o_type == KD_FA_TYPE_F32) {
+#pragma unroll
+            for (int dblk = 0; dblk < 4; ++dblk) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x4 v = {o[dblk][4 * g] * inv, o[dblk][4 * g + 1] * inv, o[dblk][4 * g + 2] * inv,
+                                     o[dblk][4 * g + 3] * inv};
+                    *reinterpret_cast<__attribute__((address_space(3))) f32x4 *>(
+                        sRaw + r32 * 128 + (((2 * g + h2) ^ (r32 & 7)) << 4)) = v;
+                }
+                flush(dblk * 128);
+            }
+        } else {
+            const bool bf = ap->o_type == KD_FA_TYPE_BF16;
+#pragma unroll
+            for (int rnd = 0; rnd < 2; ++rnd) {
+#pragma unroll
+                for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int dblk = 2 * rnd + dd;
+                        const float v0 = o[dblk][4 * g] * inv, v1 = o[dblk][4 * g + 1] * inv;
+                        const float v2 = o[dblk][4 * g + 2] * inv, v3 = o[dblk][4 * g + 3] * inv;
+                        const u32x2 w = bf ? (u32x2){Elem<__bf16>::pack2(v0, v1), Elem<__bf16>::pack2(v2, v3)}
+                                           : (u32x2){Elem<_Float16>::pack2(v0, v1), Elem<_Float16>::pack2(v2, v3)};
+                        *reinterpret_cast<__attribute__((address_space(3))) u32x2 *>(
+                            sRaw + r32 * 128 + (((dd * 4 + g) ^ (r32 & 7)) << 4) + 8 * h2) = w;
+                    }
+                flush(rnd * 128);
+            }
+        }
+    };
+
+    // ---- the first unit: Q from memory, K(0), V(0), K(1) ---------------------------
+    Unit cur = unit_at(u);
+    {
+        const int q_row = cur.row0 + wave * 32 + l32;
+        const int bh = u / a.n_qt;
+        load_q_frags<T, KD_FA_ROPE_NONE>(a, q_row < Lq ? q_row : Lq - 1, bh % a.H, bh / a.H, hi, qf);
+    }
+    u += wpx;
+    bool has_nxt = u < u_end;
+    Unit nxt = has_nxt ? unit_at(u) : cur;
+    issue_k(cur.k, 0, sK0);
+    issue_v(cur.v, 0, sV0);
+    issue_k(cur.k, 1, sK1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    // the previous unit's O stores were all issued after this unit's V(0):
+    // its first wait then counts them (16 with F32 O, 8 with 16-bit O)
+    int n_after = 0;
+
+    for (;;) {
+        // ---- the unit: the scores of tile 0 (K(0) in its buffer), then the
+        // pipelined steps of fa_fwd_d128 --------------------------------------------
+        f32x16 sa0, sa1, sb0, sb1;   // scores of the tiles of even / odd index
+        qk(sK0, sa0, sa1);
+        // V(0) is in, and every wave is done with K(0) before K(2) lands in
+        // its buffer
+        if (n_after == 16)
+            asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        else if (n_after == 8)
+            asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        {
+            float q[32];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) { q[i] = sa0[i]; q[16 + i] = sa1[i]; }
+            m_run = __builtin_fmaxf(m_run, pair_max(max32_mfma(q)) * c2);
+        }
+        // step t: softmax and PV of tile t (scores c0, c1; V(t) at vs_) and,
+        // when NEXT, the scores n0, n1 of tile t+1 (K at kn_); DMAs of V(t+1)
+        // into dV and K(t+2) into dK.  The last step (!NEXT) fetches the next
+        // unit's K(0), K(1) instead.  TAIL: tile t is the last, partial one.
+        auto pstep = [&](auto next_c, auto tail_c, int t, const f32x16 &c0, const f32x16 &c1, f32x16 &n0,
+                         f32x16 &n1, const lds_t *kn_, const lds_t *vs_, lds_t *dK, lds_t *dV)
+                         __attribute__((always_inline)) {
+            constexpr bool NEXT = decltype(next_c)::value;
+            constexpr bool TAIL = decltype(tail_c)::value;
+            if (has_nxt) {
+                if (t >= 1 && t <= kPieces) convert_piece(t - 1);
+                if (t < kPieces) {
+                    // the raw area is read (above, or by the previous unit's
+                    // O staging) before the DMA refills it
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    issue_piece(nxt, t);
+                }
+            }
+            if (NEXT) {
+                issue_v(cur.v, t + 1, dV);
+                if (t + 2 < n_tiles) issue_k(cur.k, t + 2, dK);
+            } else if (has_nxt) {
+                issue_k(nxt.k, 0, sK0);
+                issue_k(nxt.k, 1, sK1);
+            }
+            const int key0 = t * kBN;
+            auto drop_tail = [&](float *p) __attribute__((always_inline)) {
+                if (TAIL) {
+                    // key key0 + 8 hi + off of this lane is below Lk
+                    const int lim = Lk - key0 - 8 * (fresh_lane() >> 5);
+#pragma unroll
+                    for (int i = 0; i < 32; ++i) {
+                        const int off = (i >> 4) * 32 + 16 * ((i >> 3) & 1) + (i & 7);
+                        p[i] = off < lim ? p[i] : 0.0f;
+                    }
+                }
+            };
+            vec8 pb[4];
+            float p[32];
+            float nm = -m_run;
+            vec8 ka[8][2];
+            if (NEXT) {
+                n0 = (f32x16){};
+                n1 = (f32x16){};
+#pragma unroll
+                for (int ks = 0; ks < kKPre; ++ks) {
+                    ka[ks][0] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(kn_ + k_rd[ks]);
+                    ka[ks][1] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(kn_ + k_rd[ks] + 32 * 256);
+                }
+#pragma unroll
+                for (int ks = 0; ks < 8; ++ks) {
+                    if (ks + kKPre < 8) {
+                        ka[ks + kKPre][0] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(kn_ + k_rd[ks + kKPre]);
+                        ka[ks + kKPre][1] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(kn_ + k_rd[ks + kKPre] + 32 * 256);
+                    }
+                    n0 = E::mfma(ka[ks][0], qf[ks], n0);
+                    n1 = E::mfma(ka[ks][1], qf[ks], n1);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(c0[i], c2, nm));
+                p[16 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(c1[i], c2, nm));
+            }
+            drop_tail(p);
+            float sum = pack_sum(p, pb);
+            if (NEXT) sched_pipe<kKPre, kPipeVpm>();
+            const float pair = pair_sum(sum);
+            if (__builtin_amdgcn_ballot_w64(!(pair <= E::kSumCap)) != 0) {
+                float q[32];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) { q[i] = c0[i]; q[16 + i] = c1[i]; }
+                move_max(pair_max(max32_mfma(q)) * c2, !(pair <= E::kSumCap));
+                nm = -m_run;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(c0[i], c2, nm));
+                    p[16 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(c1[i], c2, nm));
+                }
+                drop_tail(p);
+                sum = pack_sum(p, pb);
+            }
+            l_half += sum;
+            pv(vs_, pb);
+            if (NEXT || has_nxt) {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __syncthreads();
+            }
+        };
+        // steps 0 .. n_tiles-2 have a next tile (and are full tiles); step t:
+        // K(t+1) in sK[(t+1)&1], V(t) in sV[t&1]
+        const bool tail = Lk % kBN != 0;
+        int t = 0;
+        for (; t + 2 < n_tiles; t += 2) {
+            pstep(BC<true>(), BC<false>(), t, sa0, sa1, sb0, sb1, sK1, sV0, sK0, sV1);
+            pstep(BC<true>(), BC<false>(), t + 1, sb0, sb1, sa0, sa1, sK0, sV1, sK1, sV0);
+        }
+        if (t + 1 < n_tiles) {   // two steps left: t (even) and t+1 (last)
+            pstep(BC<true>(), BC<false>(), t, sa0, sa1, sb0, sb1, sK1, sV0, sK0, sV1);
+            if (tail)
+                pstep(BC<false>(), BC<true>(), t + 1, sb0, sb1, sa0, sa1, sK0, sV1, sK1, sV0);
+            else
+                pstep(BC<false>(), BC<false>(), t + 1, sb0, sb1, sa0, sa1, sK0, sV1, sK1, sV0);
+        } else {   // one step left: t (even, last)
+            if (tail)
+                pstep(BC<false>(), BC<true>(), t, sa0, sa1, sb0, sb1, sK1, sV0, sK0, sV1);
+            else
+                pstep(BC<false>(), BC<false>(), t, sa0, sa1, sb0, sb1, sK1, sV0, sK0, sV1);
+        }
+        // ---- the next unit's V(0), then this unit's O -------------------------
+        if (has_nxt) issue_v(nxt.v, 0, sV0);
+        asm volatile("" ::: "memory");
+        flush_unit(cur);
+        if (!has_nxt) break;
+        n_after = cur.row0 + kLRows <= Lq ? (a.o_type == KD_FA_TYPE_F32 ? 16 : 8) : 0;
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks)
+            qf[ks] = *reinterpret_cast<const __attribute__((address_space(3))) vec8 *>(sQf + ks * 1024 + lane * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = (f32x16){};
+        m_run = -INFINITY;
+        l_half = 0.0f;
+        cur = nxt;
+        u += wpx;
+        has_nxt = u < u_end;
+        if (has_nxt) nxt = unit_at(u);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // mask_live_kernel: the mask summary of fa_fwd_xres.  One wave per (mask
 // batch, mask head, 32-row query block); each load instruction reads whole
 // rows: lane l takes 16-byte chunk l % 32 (keys 8 (l % 32) .. +7, tile
@@ -1626,6 +2137,24 @@ hipError_t launch_xres(const Args &a, int kv_type, hipStream_t s) {
         launch_xres_t<__bf16>(a, s);
     else
         launch_xres_t<_Float16>(a, s);
+    return hipGetLastError();
+}
+
+template <typename T>
+static void launch_xlong_t(const Args &a, hipStream_t s) {
+    // at most one workgroup per CU (256), a multiple of the 8 XCDs
+    const int g = a.n_blocks < 256 ? (a.n_blocks + 7) / 8 * 8 : 256;
+    if (a.q_type == KD_FA_TYPE_F32)
+        hipLaunchKernelGGL((fa_fwd_xlong<T, true>), dim3(g), dim3(64 * kLWaves), 0, s, a);
+    else
+        hipLaunchKernelGGL((fa_fwd_xlong<T, false>), dim3(g), dim3(64 * kLWaves), 0, s, a);
+}
+
+hipError_t launch_xlong(const Args &a, int kv_type, hipStream_t s) {
+    if (kv_type == KD_FA_TYPE_BF16)
+        launch_xlong_t<__bf16>(a, s);
+    else
+        launch_xlong_t<_Float16>(a, s);
     return hipGetLastError();
 }
 

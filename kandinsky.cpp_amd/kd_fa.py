@@ -63,6 +63,7 @@ ROUTE_NO_SPLIT = 8
 ROUTE_W64_SHORT = 16
 ROUTE_STAGED = 32
 ROUTE_SUMMARY = 64
+ROUTE_NO_XLONG = 128
 
 
 class KdFaTensor(ctypes.Structure):

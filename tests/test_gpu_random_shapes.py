@@ -5,8 +5,9 @@ and batch broadcast of K/V), the operand types (K/V F16 or BF16, Q F32 or in
 K's type), a mask (none, a per-batch padding mask, or random finite values
 with -inf holes), and a scale (positive or negative), then runs the node
 under each routing choice of kd_fa_set_routing: as routed, with the 64-row
-kernel out, with the short-key kernel out, with the 64-row kernel taking the
-short unmasked key sets too, and with both specialised kernels out.  Every
+and long-prompt kernels out, with the short-key kernel out, with the 64-row
+kernel taking the short unmasked key sets too, and with all specialised
+kernels out.  Every
 kernel computes each query row with the same arithmetic, so all outputs must
 be bitwise equal; the routed one must also match the float64 oracle on every
 row.  Odd seeds give the mask rows whole 8-key chunks (ggml pads them; the
@@ -43,8 +44,8 @@ def _case(seed):
     Hkv = int(rng.choice([h for h in (1, 2, 4) if H % h == 0]))
     Lq = int(rng.integers(1, 301))
     # key counts in each kernel's range: < 64, the short-key kernel's, the
-    # 4-wave 32-row kernel's (unmasked) and the 64-row kernel's
-    bins = [(1, 64), (64, 257), (257, 897), (897, 1501)]
+    # long-prompt kernel's (unmasked) and the 64-row kernel's
+    bins = [(1, 64), (64, 257), (257, 1025), (1025, 1501)]
     lo, hi = bins[seed % 4]
     Lk = int(rng.integers(lo, hi))
     kv = [torch.float16, torch.bfloat16][int(rng.integers(2))]
