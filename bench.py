@@ -52,6 +52,9 @@ def parse():
                         "and print its ms per call (for counter runs)")
     p.add_argument("--cross-only", action="store_true",
                    help="only the text cross-attention (C2 shape): for counter runs of its kernel")
+    p.add_argument("--cross-long-only", action="store_true",
+                   help="only the long-prompt cross-attention in the reference's operand form (Q F32 "
+                        "[128, 31744, 32, 2], K/V F16 with 512 keys, no mask): for counter runs of its kernel")
     p.add_argument("--hbm-ceiling", action="store_true",
                    help="only torch's bf16 -> F32 copy at the cross-attention's sizes (its Q-in / O-out "
                         "byte mix) and a 1 GiB F32 copy")
@@ -299,6 +302,15 @@ def main():
         wsx = torch.empty(max(kd_fa.workspace_size_full(dx), 16), dtype=torch.uint8, device=dev)
         msx = time_launches(torch, lambda: kd_fa.run_desc(dx, None, stream, wsx), args.steps, args.warmup, stream)
         print(json.dumps({"cross_attn_ms": round(msx, 4)}))
+        return
+    if args.cross_long_only:
+        ql = rand(torch, (B, HEADS, L, D), 3, dev, torch.float32)
+        kl = rand(torch, (B, HEADS, 512, D), 1612, dev, torch.float16)
+        vl = rand(torch, (B, HEADS, 512, D), 2612, dev, torch.float16)
+        ol = torch.empty((B, L, HEADS, D), device=dev, dtype=torch.float32)
+        dlong = kd_fa.make_desc(ql, kl, vl, None, ol, 1.0 / D ** 0.5)
+        msl = time_launches(torch, lambda: kd_fa.run_desc(dlong, None, stream), args.steps, args.warmup, stream)
+        print(json.dumps({"cross_attn_long_512_ms": round(msl, 4)}))
         return
     if args.linear_only:
         import kd_mm
