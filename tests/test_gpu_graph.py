@@ -8,9 +8,10 @@ calls -- so a replay must give exactly the eager calls' result.  Captured
 here: the self-attention with RoPE and no workspace (kd_fa_rope_run, whose
 staged schedule is a sequence of K pre-pass + attention launches), the same
 through the allocation-free kd_fa_dit_run_static (query/key RMSNorm, K in
-the library's static array), the masked text cross-attention (kd_fa_run)
-and a Q8_0 linear layer through a workspace (kd_mm_run: weight expansion +
-product).  The graph is replayed several times with eager work of the
+the library's static array), the masked text cross-attention (kd_fa_run),
+the unmasked cross-attention of a long prompt (the persistent kernel, four
+query tiles per workgroup) and a Q8_0 linear layer through a workspace
+(kd_mm_run: weight expansion + product).  The graph is replayed several times with eager work of the
 program between the replays, the inputs are rewritten in place between
 replays, and every replay is compared bitwise with the eager calls on the
 same inputs."""
@@ -49,6 +50,11 @@ class Layer:
         self.kx = torch.empty((B, H, 100, D), dtype=torch.bfloat16, device=DEV)
         self.vx = torch.empty_like(self.kx)
         self.mask = torch.full((B, 1, L, 104), float("-inf"), dtype=torch.float16, device=DEV)
+        # a long prompt's cross-attention: 2 x 16 heads x 32 query tiles of
+        # 256 rows = 1,024 units, four per workgroup of the persistent kernel
+        self.ql = torch.empty((B, 16, 8192, D), dtype=torch.bfloat16, device=DEV)
+        self.kl = torch.empty((B, 16, 300, D), dtype=torch.bfloat16, device=DEV)
+        self.vl = torch.empty_like(self.kl)
         self.mask[0, :, :, :77] = 0
         self.mask[1, :, :, :31] = 0
         table = kd_fa.visual_rope_table(T, Hp, Wp, AXES, SCALE_FACTOR, THETA)
@@ -68,10 +74,11 @@ class Layer:
         return {"self": torch.empty((B, L, H, D), device=DEV),
                 "static": torch.empty((B, L, H, D), device=DEV),
                 "cross": torch.empty((B, L, H, D), device=DEV),
+                "long": torch.empty((B, 8192, 16, D), device=DEV),
                 "linear": torch.empty((L, 256), device=DEV)}
 
     def fill(self, seed):
-        for j, t in enumerate((self.q, self.k, self.v, self.kx, self.vx)):
+        for j, t in enumerate((self.q, self.k, self.v, self.kx, self.vx, self.ql, self.kl, self.vl)):
             t.copy_(randn(tuple(t.shape), torch.bfloat16, seed + j))
         self.x.copy_(randn(tuple(self.x.shape), torch.float32, seed + 9))
 
@@ -82,6 +89,7 @@ class Layer:
         d_self = kd_fa.make_desc(self.q, self.k, self.v, None, out["self"], s)
         d_static = kd_fa.make_desc(self.q, self.k, self.v, None, out["static"], s)
         d_cross = kd_fa.make_desc(self.q, self.kx, self.vx, self.mask, out["cross"], s)
+        d_long = kd_fa.make_desc(self.ql, self.kl, self.vl, None, out["long"], s)
         d_lin = kd_mm.make_desc(self.wq8, self.x, self.bias, out["linear"])
         ws = torch.empty(max(kd_mm.workspace_size(d_lin), 16), dtype=torch.uint8, device=DEV)
 
@@ -89,14 +97,15 @@ class Layer:
             assert kd_fa.run_desc(d_self, self.rope) == kd_fa.OK
             assert kd_fa.run_static(d_static, self.rope, self.norm) == kd_fa.OK
             assert kd_fa.run_desc(d_cross) == kd_fa.OK
+            assert kd_fa.run_desc(d_long) == kd_fa.OK
             assert kd_mm.run_desc(d_lin, ws) == 0
 
-        return run, (d_self, d_static, d_cross, d_lin, ws)
+        return run, (d_self, d_static, d_cross, d_long, d_lin, ws)
 
 
 def test_layer_calls_replay_bitwise():
     _need_gpu()
-    _announce("graph capture: staged rope_run, dit_run_static, masked cross-attn, q8_0 linear")
+    _announce("graph capture: staged rope_run, dit_run_static, masked cross-attn, long-prompt cross-attn, q8_0 linear")
     # this shape fits one round of workgroups, where kd_fa_rope_run would be
     # one on-load launch: ROUTE_STAGED keeps its staged launch sequence
     with kd_fa.routing(kd_fa.ROUTE_STAGED):
