@@ -1510,6 +1510,9 @@ void fa_fwd_xlong(Args a) {
                 const u32x4 w = {E::pack2(x0.x, x0.y) ^ ng, E::pack2(x0.z, x0.w) ^ ng, E::pack2(x1.x, x1.y) ^ ng,
                                  E::pack2(x1.z, x1.w) ^ ng};
                 *reinterpret_cast<__attribute__((address_space(3))) u32x4 *>(sQf + (2 * p + e) * 1024 + ln * 16) = w;
+                // both reads have returned before what follows (the next
+                // piece's DMA into the raw area)
+                asm volatile("" ::"v"(x0.w), "v"(x1.w));
             }
         } else {
 #pragma unroll
@@ -1520,6 +1523,7 @@ void fa_fwd_xlong(Args a) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) w[j] = E::pack2(E::lo(r[j]), E::hi(r[j])) ^ ng;
                 *reinterpret_cast<__attribute__((address_space(3))) u32x4 *>(sQf + (4 * p + e) * 1024 + ln * 16) = w;
+                asm volatile("" ::"v"(r[3]));   // the read has returned
             }
         }
     };
@@ -1706,21 +1710,20 @@ void fa_fwd_xlong(Args a) {
                          __attribute__((always_inline)) {
             constexpr bool NEXT = decltype(next_c)::value;
             constexpr bool TAIL = decltype(tail_c)::value;
-            if (has_nxt) {
-                if (t >= 1 && t <= kPieces) convert_piece(t - 1);
-                if (t < kPieces) {
-                    // the raw area is read (above, or by the previous unit's
-                    // O staging) before the DMA refills it
-                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                    issue_piece(nxt, t);
-                }
-            }
             if (NEXT) {
                 issue_v(cur.v, t + 1, dV);
                 if (t + 2 < n_tiles) issue_k(cur.k, t + 2, dK);
             } else if (has_nxt) {
                 issue_k(nxt.k, 0, sK0);
                 issue_k(nxt.k, 1, sK1);
+            }
+            if (has_nxt) {
+                // the raw area's reads (the conversion's, which end in
+                // registers the DMA is ordered after, or the previous unit's
+                // O staging, consumed by its stores) come before the DMA
+                // refills it
+                if (t >= 1 && t <= kPieces) convert_piece(t - 1);
+                if (t < kPieces) issue_piece(nxt, t);
             }
             const int key0 = t * kBN;
             auto drop_tail = [&](float *p) __attribute__((always_inline)) {
