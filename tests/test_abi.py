@@ -444,3 +444,19 @@ def test_static_entry_point_refuses_oversize_f32_before_device_work():
     bad = kd_fa.make_desc(q, k, k, None, dst, 0.1, max_bias=1.0)
     assert lib.kd_fa_dit_run_static(ctypes.byref(bad), ctypes.byref(rope), None, None) == kd_fa.ERR_PARAM
     assert b"static scratch" in lib.kd_fa_strerror(kd_fa.ERR_SCRATCH)
+
+
+def test_python_constants_equal_the_header():
+    """Every KD_FA_<NAME> = <value> enumerator and KD_FA_ABI_VERSION of
+    include/kd_fa.h has the same value as kd_fa.<NAME> (the ctypes mirror),
+    and the mirror defines no routing flag the header lacks."""
+    import re
+    text = open(kd_fa.HEADER_PATH).read()
+    enums = {m.group(1): int(m.group(2)) for m in re.finditer(r"\bKD_FA_([A-Z0-9_]+)\s*=\s*(-?\d+)", text)}
+    assert len(enums) >= 25
+    for name, value in enums.items():
+        assert getattr(kd_fa, name) == value, name
+    abi = re.search(r"#define\s+KD_FA_ABI_VERSION\s+(\d+)", text)
+    assert abi and int(abi.group(1)) == kd_fa.ABI_VERSION
+    mirrored = {n for n in dir(kd_fa) if n.startswith("ROUTE_")}
+    assert mirrored == {n for n in enums if n.startswith("ROUTE_")}

@@ -72,3 +72,13 @@ def test_run_validates_before_touching_the_device():
     assert kd_mm._lib().kd_mm_run(ctypes.byref(d), None, 0, None) == kd_fa.ERR_TYPE
     t = kd_mm.w_view(w)
     assert kd_mm._lib().kd_mm_dequant(ctypes.byref(t), None, 0, None) == kd_fa.ERR_NULL
+
+
+def test_python_type_ids_equal_the_header():
+    """The KD_MM_TYPE_* ids of include/kd_mm.h are kd_mm.TYPE_* (the ctypes mirror)."""
+    import re
+    text = open(kd_mm.HEADER_PATH).read()
+    ids = {m.group(1): int(m.group(2)) for m in re.finditer(r"\bKD_MM_(TYPE_[A-Z0-9_]+)\s*=\s*(-?\d+)", text)}
+    assert len(ids) == 5
+    for name, value in ids.items():
+        assert getattr(kd_mm, name) == value, name
