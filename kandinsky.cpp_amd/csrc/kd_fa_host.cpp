@@ -857,7 +857,7 @@ const char *kd_fa_strerror(int status) {
     }
 }
 
-int kd_fa_version(void) { return 300; }
+int kd_fa_version(void) { return 301; }
 
 int kd_fa_abi_version(void) { return KD_FA_ABI_VERSION; }
 
