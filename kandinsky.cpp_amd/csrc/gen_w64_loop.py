@@ -557,10 +557,12 @@ class Gen:
         tr.out.extend(tb.out[n0:])
         tr.label(skip)
 
-    def step(self, tr, p, final, tag, toff=0):
+    def step(self, tr, p, final, tag, toff=0, unit=False):
         """Step t = S_T + toff with parity p: S(t) in S[p], K(t+1) in
         KBUF[1-p], V(t) in VBUF[p]; P[p] holds the weights of keys 0-31 of
-        tile t."""
+        tile t.  unit: a step of the persistent kernel's unit block (the
+        next unit's Q pieces in steps 0-4; the last step fetches the next
+        unit's K(0) and K(1))."""
         q = 1 - p
         vpre, vseq = self.pv_stream(VBUF[p], p)
 
@@ -568,6 +570,8 @@ class Gen:
             for r in vpre:
                 tr.emit(r)
             self.check(tr, p, tag)
+            if unit and final:
+                self.piece_block(tr, p, toff, tag)
 
         if not final:
             pre, seq = self.qk_stream(KBUF[q], q)
@@ -589,13 +593,20 @@ class Gen:
             else:
                 self.merge(tr, seq, self.softmax_half(p, p, 1, (0, 1), True), dmas, PER1, tail, CHECK_AT)
         else:
+            if unit:
+                self.next_k(tr)
             for x in self.softmax_half(p, p, 1, (0, 1), True):
                 tr.emit(x)
             tail(tr)
         if not final:
             self.mask_tail(tr, q, toff, tag)
+            if unit:
+                self.piece_block(tr, p, toff, tag)
             self.merge(tr, vseq, self.softmax_half(q, q, 0, (0, 1), True))
-            tr.raw("s_waitcnt vmcnt(0)")
+            if unit:
+                self.step_wait(tr, toff, tag)
+            else:
+                tr.raw("s_waitcnt vmcnt(0)")
             tr.raw("s_barrier")
             tr.settle()
         else:
@@ -694,7 +705,375 @@ class Gen:
         return lines
 
 
-def check_registers(lines):
+# ------------------------------------------------- persistent unit block
+# fa_fwd_xlong64 (kd_fa_kernel.hip) runs the loop above once per unit of 256
+# query rows of one (b, h) and walks several units per workgroup; its block
+# adds, per unit, the next unit's Q (F32 rows brought in by DMA during the
+# first steps and rounded into the Q fragment area), the next unit's first
+# K/V tiles (issued by the last step and after it) and the O epilogue
+# (normalised rows staged in LDS, stored as whole 128-byte lines through a
+# buffer resource whose record count ends at the last valid row).
+XL_QF = 65536          # Q fragments: per wave 16 KiB (the loop's Q_OFF layout)
+XL_RAW = 131072        # per wave 8 KiB: raw Q pieces in the loop, O staging after it
+XL_RAW_W = 8192
+XL_PIECES = 4          # 128-byte pieces of an F32 row, one per step in steps 0-3
+XL_PIECE_DMAS = 8      # DMA instructions per piece and wave
+XL_KV_DMAS = 8         # K/V DMA instructions per step and wave (the last step: K(0), K(1) of the next unit)
+XL_PITCH = 144         # O staging: bytes per row (128 + 16: no bank conflicts)
+S_NQ = 80              # s[80:83] the next unit's Q buffer resource
+S_T2, S_T3 = 96, 97    # temporaries of the unit block
+XL_S_FIRST, XL_S_LAST = 80, 97
+# epilogue VGPRs (the loop's are free by then, except the half-row sums LH)
+EP_INV = (216, 217)
+EP_T = list(range(218, 228))
+EP_LANE = 228
+EP_STW, EP_STW16, EP_STR, EP_OOFF = 229, 234, 232, 233
+EP_OROW = list(range(240, 248))
+XL_STORES = {"f32": 32, "b16": 16}   # O stores per wave and unit
+
+
+def _xl_unit_methods():
+    """Methods of Gen for the unit block (kept apart from the loop's)."""
+
+    def next_k(self, tr):
+        """The last step of a unit: the next unit's K(0) and K(1) into the K
+        buffers (no wave reads them any more: the previous step's barrier has
+        passed); record count 0 when there is no next unit (zeros)."""
+        for j, w in enumerate(("nkw0", "nkw1", "nkw2", "rw3")):
+            tr.emit(Ins(f"s_mov_b32 s{S_K + j}, %[{w}]", "salu"))
+        for j in range(4):
+            for x in self.dma("k", KBUF[0], j):
+                tr.emit(x)
+        for x in self.advance("k"):
+            tr.emit(x)
+        for j in range(4):
+            for x in self.dma("k", KBUF[1], j):
+                tr.emit(x)
+
+    def piece_index(self, tr, toff):
+        """s[S_T2] = the step index t = S_T + toff."""
+        if toff:
+            tr.raw(f"s_add_u32 s{S_T2}, s{S_T}, {toff}")
+        else:
+            tr.raw(f"s_mov_b32 s{S_T2}, s{S_T}")
+
+    def step_wait(self, tr, toff, tag):
+        """The end of a non-final step t: its K/V DMAs done.  In steps 0-3
+        the piece DMAs issued after them (XL_PIECE_DMAS) stay in flight:
+        the conversion a step later waits for them, so that their memory
+        latency overlaps a whole step."""
+        w0, wd = f".Lxl_w0_{tag}_%=", f".Lxl_wd_{tag}_%="
+        self.piece_index(tr, toff)
+        tr.raw(f"s_cmp_lt_u32 s{S_T2}, {XL_PIECES}")
+        tr.raw(f"s_cbranch_scc0 {w0}")
+        tr.raw(f"s_waitcnt vmcnt({XL_PIECE_DMAS})")
+        tr.raw(f"s_branch {wd}")
+        tr.label(w0)
+        tr.raw("s_waitcnt vmcnt(0)")
+        tr.label(wd)
+
+    def piece_block(self, tr, p, toff, tag):
+        """In step t = S_T + toff, t <= 4: piece t - 1 of the next unit's Q
+        rows (t >= 1) from the raw area, rounded to the operand type (with
+        load_q_frags' sign for scale < 0) into the fragment area; then the
+        DMA of piece t (t <= 3) into the raw area, which the conversion's
+        reads have left.  Piece p of a row is its bytes 128 p .. +127 (k-steps
+        2 p and 2 p + 1); DMA instruction i = 4 qb + 2 kk + j of a piece puts
+        lane l's 16 bytes of row 32 qb + l % 32, bytes 128 p + 64 kk +
+        32 (l / 32) + 16 j, at raw + 1024 i + 16 l.  The block uses the dead
+        score registers S[p]; it ends with no LDS operation pending, so the
+        tracker may go on as on the path that skips it."""
+        R = S_BASE[p]
+        skip, noconv = f".Lxl_nopiece_{tag}_%=", f".Lxl_noconv_{tag}_%="
+        self.piece_index(tr, toff)
+        tr.raw(f"s_cmp_gt_u32 s{S_T2}, {XL_PIECES}")
+        tr.raw(f"s_cbranch_scc1 {skip}")
+        tr.raw("s_waitcnt lgkmcnt(0)")
+        tr.raw(f"s_cmp_eq_u32 s{S_T2}, 0")
+        tr.raw(f"s_cbranch_scc1 {noconv}")
+        # conversion of piece t - 1, whose DMAs were issued before this
+        # step's K/V DMAs (XL_KV_DMAS of them since)
+        tr.raw(f"s_waitcnt vmcnt({XL_KV_DMAS})")
+        tr.raw(f"s_sub_u32 s{S_T3}, s{S_T2}, 1")
+        tr.raw(f"s_lshl_b32 s{S_T3}, s{S_T3}, 11")
+        tr.raw(f"v_add_u32 {vr(R + 32)}, %[rawdelta], %[qrd]")
+        tr.raw(f"v_add_u32 {vr(R + 33)}, s{S_T3}, %[qrd]")
+        for i in range(8):
+            tr.raw(f"ds_read_b128 {vrng(R + 4 * i, 4)}, {vr(R + 32)} offset:{1024 * i}")
+        tr.raw("s_waitcnt lgkmcnt(0)")
+        for qb in range(2):
+            for kk in range(2):
+                j0, j1 = R + 4 * (4 * qb + 2 * kk), R + 4 * (4 * qb + 2 * kk + 1)
+                w = R + 36 + 4 * (2 * qb + kk)
+                srcs = ((j0, j0 + 1), (j0 + 2, j0 + 3), (j1, j1 + 1), (j1 + 2, j1 + 3))
+                for x, (a, b) in enumerate(srcs):
+                    tr.raw(f"{self.cvt} {vr(w + x)}, {vr(a)}, {vr(b)}")
+                for x in range(4):
+                    tr.raw(f"v_xor_b32 {vr(w + x)}, %[qsgn], {vr(w + x)}")
+                tr.raw(f"ds_write_b128 {vr(R + 33)}, {vrng(w, 4)} offset:{1024 * (8 * qb + kk)}")
+        tr.raw("s_waitcnt lgkmcnt(0)")
+        tr.label(noconv)
+        # DMA of piece t
+        tr.raw(f"s_cmp_ge_u32 s{S_T2}, {XL_PIECES}")
+        tr.raw(f"s_cbranch_scc1 {skip}")
+        tr.raw(f"s_lshl_b32 s{S_T2}, s{S_T2}, 7")
+        for qb in range(2):
+            for kk in range(2):
+                for j in range(2):
+                    i = 4 * qb + 2 * kk + j
+                    tr.raw(f"s_add_u32 s{S_T3}, s{S_T2}, {64 * kk + 16 * j}")
+                    tr.raw(f"v_add_u32 {vr(R + 52 + i)}, s{S_T3}, %[qoff{qb}]")
+                    tr.raw(f"s_add_u32 m0, %[rawb], {1024 * i}")
+                    tr.raw("s_nop 0")
+                    tr.raw(f"buffer_load_dwordx4 {vr(R + 52 + i)}, s[{S_NQ}:{S_NQ + 3}], 0 offen lds")
+        tr.label(skip)
+
+    def epilogue(self, tr):
+        """After the last step: V(0) of the next unit once every wave is
+        done with the V buffers, then O / l of the unit's rows as whole
+        lines (store_o_row_l's arithmetic: l the sum over the lane pair,
+        O * (l == 0 ? 0 : 1 / l) with the correctly rounded division)."""
+        e = tr.emit
+        tr.raw("s_barrier")
+        for j, w in enumerate(("nvw0", "nvw1", "nvw2", "rw3")):
+            e(Ins(f"s_mov_b32 s{S_V + j}, %[{w}]", "salu"))
+        for j in range(4):
+            for x in self.dma("v", VBUF[0], j):
+                e(x)
+        t = EP_T
+        for qb in range(2):
+            e(valu(f"v_mov_b32 {vr(X)}, {vr(LH[qb])}", {vr(LH[qb])}, {vr(X)}))
+            e(valu(f"v_mov_b32 {vr(Y)}, {vr(LH[qb])}", {vr(LH[qb])}, {vr(Y)}))
+            e(Ins(f"v_permlane32_swap_b32 {vr(X)}, {vr(Y)}", "perm", {vr(X), vr(Y)}, {vr(X), vr(Y)}))
+            lv, d, r, n, q, er, inv = (vr(t[0]), vr(t[1]), vr(t[2]), vr(t[3]), vr(t[4]), vr(t[5]),
+                                       vr(EP_INV[qb]))
+            e(valu(f"v_add_f32 {lv}, {vr(X)}, {vr(Y)}", {vr(X), vr(Y)}, {lv}))
+            e(valu(f"v_div_scale_f32 {d}, s[{S_VCC}:{S_VCC + 1}], {lv}, {lv}, 1.0", {lv}, {d}))
+            e(Ins(f"v_rcp_f32 {r}, {d}", "trans", {d}, {r}))
+            e(valu(f"v_div_scale_f32 {n}, vcc, 1.0, {lv}, 1.0", {lv}, {n}))
+            e(valu(f"v_fma_f32 {q}, -{d}, {r}, 1.0", {d, r}, {q}))
+            e(valu(f"v_fma_f32 {r}, {q}, {r}, {r}", {q, r}, {r}))
+            e(valu(f"v_mul_f32 {q}, {n}, {r}", {n, r}, {q}))
+            e(valu(f"v_fma_f32 {er}, -{d}, {q}, {n}", {d, q, n}, {er}))
+            e(valu(f"v_fma_f32 {q}, {er}, {r}, {q}", {er, r, q}, {q}))
+            e(valu(f"v_fma_f32 {d}, -{d}, {q}, {n}", {d, q, n}, {d}))
+            tr.raw("s_nop 3", 4)
+            e(valu(f"v_div_fmas_f32 {d}, {d}, {r}, {q}", {d, r, q}, {d}))
+            e(valu(f"v_div_fixup_f32 {inv}, {d}, {lv}, 1.0", {d, lv}, {inv}))
+            e(valu(f"v_cmp_neq_f32 vcc, 0, {lv}", {lv}, ()))
+            e(valu(f"v_cndmask_b32 {inv}, 0, {inv}, vcc", {inv}, {inv}))
+        # lane addresses: staging write (row l % 32, F32 chunk 2 g + l / 32 /
+        # 16-bit 8-byte half), staging read (row 8 j + l / 8, chunk l % 8),
+        # global row offset ((l / 8) rows, chunk l % 8) per 8-row block
+        ln, a0, a1 = vr(EP_LANE), vr(t[6]), vr(t[7])
+        e(valu(f"v_mbcnt_lo_u32_b32 {ln}, -1, 0", (), {ln}))
+        e(valu(f"v_mbcnt_hi_u32_b32 {ln}, -1, {ln}", {ln}, {ln}))
+        e(valu(f"v_and_b32 {a0}, 31, {ln}", {ln}, {a0}))
+        e(valu(f"v_mul_u32_u24 {a0}, {XL_PITCH}, {a0}", {a0}, {a0}))
+        e(valu(f"v_add_u32 {a0}, %[rawb], {a0}", {a0}, {a0}))
+        e(valu(f"v_lshrrev_b32 {a1}, 5, {ln}", {ln}, {a1}))
+        e(valu(f"v_lshl_add_u32 {vr(EP_STW)}, {a1}, 4, {a0}", {a1, a0}, {vr(EP_STW)}))
+        e(valu(f"v_lshl_add_u32 {vr(EP_STW16)}, {a1}, 3, {a0}", {a1, a0}, {vr(EP_STW16)}))
+        e(valu(f"v_lshrrev_b32 {a0}, 3, {ln}", {ln}, {a0}))
+        e(valu(f"v_and_b32 {a1}, 7, {ln}", {ln}, {a1}))
+        e(valu(f"v_mul_u32_u24 {vr(EP_STR)}, {XL_PITCH}, {a0}", {a0}, {vr(EP_STR)}))
+        e(valu(f"v_add_u32 {vr(EP_STR)}, %[rawb], {vr(EP_STR)}", {vr(EP_STR)}, {vr(EP_STR)}))
+        e(valu(f"v_lshl_add_u32 {vr(EP_STR)}, {a1}, 4, {vr(EP_STR)}", {a1, vr(EP_STR)}, {vr(EP_STR)}))
+        e(valu(f"v_mul_lo_u32 {a0}, %[onb2], {a0}", {a0}, {a0}))
+        e(valu(f"v_lshl_add_u32 {vr(EP_OOFF)}, {a1}, 4, {a0}", {a1, a0}, {vr(EP_OOFF)}))
+        for k in range(8):
+            tr.raw(f"s_mul_i32 s{S_T2}, %[o8], {k}")
+            e(valu(f"v_add_u32 {vr(EP_OROW[k])}, s{S_T2}, {vr(EP_OOFF)}", {vr(EP_OOFF)}, {vr(EP_OROW[k])}))
+        for j, w in enumerate(("ow0", "ow1", "ow2", "rw3")):
+            e(Ins(f"s_mov_b32 s{S_K + j}, %[{w}]", "salu"))
+        # every MFMA result has settled before the paths below read O
+        tr.raw("s_nop 7", 8)
+        tr.raw("s_nop 7", 8)
+        tr.raw("s_nop 7", 8)
+        tr.mfma_w.clear()
+        tr.raw("s_cmp_eq_u32 %[ot], 0")
+        tr.raw("s_cbranch_scc0 .Lxl_o16_%=")
+        tb = copy.deepcopy(tr)
+        n0 = len(tb.out)
+        self.store_f32(tb)
+        tr.out.extend(tb.out[n0:])
+        tr.raw("s_branch .Lxl_oend_%=")
+        tr.label(".Lxl_o16_%=")
+        tr.raw("s_cmp_eq_u32 %[ot], 1")
+        tr.raw("s_cbranch_scc0 .Lxl_of16_%=")
+        tb = copy.deepcopy(tr)
+        n0 = len(tb.out)
+        self.store_16(tb, "v_cvt_pk_bf16_f32")
+        tr.out.extend(tb.out[n0:])
+        tr.raw("s_branch .Lxl_oend_%=")
+        tr.label(".Lxl_of16_%=")
+        tb = copy.deepcopy(tr)
+        n0 = len(tb.out)
+        self.store_16(tb, "v_cvt_pk_f16_f32")
+        tr.out.extend(tb.out[n0:])
+        tr.label(".Lxl_oend_%=")
+
+    def store_f32(self, tr):
+        """F32 O: per (query block, 32-column block) the 32 rows' 128-byte
+        pieces staged, then read back 8 rows x 128 bytes per instruction and
+        stored non-temporal (O is not read again)."""
+        e = tr.emit
+        for rnd in range(8):
+            qb, dblk = divmod(rnd, 4)
+            va, rb = 24 + 32 * (rnd % 2), 120 + 16 * (rnd % 2)
+            for i in range(16):
+                a = f"a{A_O + 64 * qb + 16 * dblk + i}"
+                e(Ins(f"v_accvgpr_read_b32 {vr(va + i)}, {a}", "valu", {a}, {vr(va + i)}))
+            for i in range(16):
+                e(valu(f"v_mul_f32 {vr(va + i)}, {vr(va + i)}, {vr(EP_INV[qb])}", {vr(va + i), vr(EP_INV[qb])},
+                       {vr(va + i)}))
+            for g in range(4):
+                e(Ins(f"ds_write_b128 {vr(EP_STW)}, {vrng(va + 4 * g, 4)} offset:{32 * g}", "lds_wr",
+                      vset(va + 4 * g, 4) | {vr(EP_STW)}, ()))
+            for jr in range(4):
+                e(Ins(f"ds_read_b128 {vrng(rb + 4 * jr, 4)}, {vr(EP_STR)} offset:{8 * XL_PITCH * jr}", "lds_rd",
+                      {vr(EP_STR)}, vset(rb + 4 * jr, 4)))
+            for jr in range(4):
+                e(Ins(f"buffer_store_dwordx4 {vrng(rb + 4 * jr, 4)}, {vr(EP_OROW[4 * qb + jr])}, s[{S_K}:{S_K + 3}], "
+                      f"0 offen offset:{128 * dblk} nt", "vmem", vset(rb + 4 * jr, 4) | {vr(EP_OROW[4 * qb + jr])}, ()))
+
+    def store_16(self, tr, cvt):
+        """16-bit O: per (query block, pair of 32-column blocks) the 32 rows'
+        128-byte pieces staged, then stored as in store_f32."""
+        e = tr.emit
+        for rnd in range(4):
+            qb, dp = divmod(rnd, 2)
+            va, wp, rb = 24 + 32 * (rnd % 2), 88 + 16 * (rnd % 2), 120 + 16 * (rnd % 2)
+            for dd in range(2):
+                for i in range(16):
+                    a = f"a{A_O + 64 * qb + 16 * (2 * dp + dd) + i}"
+                    e(Ins(f"v_accvgpr_read_b32 {vr(va + 16 * dd + i)}, {a}", "valu", {a}, {vr(va + 16 * dd + i)}))
+            for i in range(32):
+                e(valu(f"v_mul_f32 {vr(va + i)}, {vr(va + i)}, {vr(EP_INV[qb])}", {vr(va + i), vr(EP_INV[qb])},
+                       {vr(va + i)}))
+            for dd in range(2):
+                for g in range(4):
+                    for h in range(2):
+                        s0 = va + 16 * dd + 4 * g + 2 * h
+                        w = wp + 8 * dd + 2 * g + h
+                        e(valu(f"{cvt} {vr(w)}, {vr(s0)}, {vr(s0 + 1)}", {vr(s0), vr(s0 + 1)}, {vr(w)}))
+            for dd in range(2):
+                for g in range(4):
+                    w = wp + 8 * dd + 2 * g
+                    e(Ins(f"ds_write_b64 {vr(EP_STW16)}, {vrng(w, 2)} offset:{64 * dd + 16 * g}", "lds_wr",
+                          vset(w, 2) | {vr(EP_STW16)}, ()))
+            for jr in range(4):
+                e(Ins(f"ds_read_b128 {vrng(rb + 4 * jr, 4)}, {vr(EP_STR)} offset:{8 * XL_PITCH * jr}", "lds_rd",
+                      {vr(EP_STR)}, vset(rb + 4 * jr, 4)))
+            for jr in range(4):
+                e(Ins(f"buffer_store_dwordx4 {vrng(rb + 4 * jr, 4)}, {vr(EP_OROW[4 * qb + jr])}, s[{S_K}:{S_K + 3}], "
+                      f"0 offen offset:{128 * dp} nt", "vmem", vset(rb + 4 * jr, 4) | {vr(EP_OROW[4 * qb + jr])}, ()))
+
+    def build_unit(self):
+        """The unit block of fa_fwd_xlong64: the loop of build() for one
+        unit, whose Q fragments are in the fragment area; the first unit of
+        a workgroup (operand first != 0) fetches its own K(0), V(0), K(1),
+        later ones find them issued by the previous unit and wait only for
+        those (the previous unit's O stores, issued after them, complete in
+        issue order)."""
+        tr = Tracker()
+        e = tr.emit
+        for qb in range(2):
+            e(valu(f"v_mov_b32 {vr(M[qb])}, 0xff800000", (), {vr(M[qb])}))
+            e(valu(f"v_mov_b32 {vr(LH[qb])}, 0", (), {vr(LH[qb])}))
+        for i in range(128):
+            e(Ins(f"v_accvgpr_write_b32 a{A_O + i}, 0", "accw", (), {f"a{A_O + i}"}))
+        for i in range(16):
+            e(Ins(f"ds_read_b128 {arng(A_Q + 4 * i, 4)}, %[qrd] offset:{1024 * i}", "lds_rd", (), aset(A_Q + 4 * i, 4)))
+        for j, w in enumerate(("kw0", "kw1", "kw2", "rw3")):
+            e(Ins(f"s_mov_b32 s{S_K + j}, %[{w}]", "salu"))
+        for j, w in enumerate(("vw0", "vw1", "vw2", "rw3")):
+            e(Ins(f"s_mov_b32 s{S_V + j}, %[{w}]", "salu"))
+        for j, w in enumerate(("nqw0", "nqw1", "nqw2", "rw3")):
+            e(Ins(f"s_mov_b32 s{S_NQ + j}, %[{w}]", "salu"))
+        tr.raw("s_cmp_eq_u32 %[first], 0")
+        tr.raw("s_cbranch_scc1 .Lxl_issued_%=")
+        for j in range(4):
+            for x in self.dma("k", KBUF[0], j):
+                e(x)
+        for x in self.advance("k"):
+            e(x)
+        for j in range(4):
+            for x in self.dma("v", VBUF[0], j):
+                e(x)
+        for x in self.advance("v"):
+            e(x)
+        for j in range(4):
+            for x in self.dma("k", KBUF[1], j):
+                e(x)
+        for x in self.advance("k"):
+            e(x)
+        tr.raw("s_waitcnt vmcnt(0)")
+        tr.raw("s_branch .Lxl_go_%=")
+        tr.label(".Lxl_issued_%=")
+        for x in self.advance("k") + self.advance("v") + self.advance("k"):
+            e(x)
+        tr.raw("s_cmp_eq_u32 %[ot], 0")
+        tr.raw("s_cbranch_scc0 .Lxl_w16_%=")
+        tr.raw(f"s_waitcnt vmcnt({XL_STORES['f32']})")
+        tr.raw("s_branch .Lxl_go_%=")
+        tr.label(".Lxl_w16_%=")
+        tr.raw(f"s_waitcnt vmcnt({XL_STORES['b16']})")
+        tr.label(".Lxl_go_%=")
+        tr.raw("s_waitcnt lgkmcnt(0)")
+        tr.lds = []
+        tr.raw("s_barrier")
+        pre, seq = self.qk_stream(KBUF[0], 0)
+        for r in pre:
+            e(r)
+        self.merge(tr, seq, [])
+        tr.raw("s_barrier")
+        for qb in range(2):
+            self.row_max(e, 0, qb, [W_BASE + i for i in range(3)])
+            e(valu(f"v_max_f32 {vr(M[qb])}, {vr(M[qb])}, {vr(X)}", {vr(M[qb]), vr(X)}, {vr(M[qb])}))
+        for x in self.softmax_half(0, 0, 0, (0, 1), True):
+            e(x)
+        tr.raw(f"s_mov_b32 s{S_T}, 0")
+        tr.label(".Lw64_loop_%=")
+        tr.raw(f"s_add_u32 s{S_TMP}, s{S_T}, 2")
+        tr.raw(f"s_cmp_lt_u32 s{S_TMP}, %[n]")
+        tr.raw(".Lw64_tail_%=".join(["s_cbranch_scc0 ", ""]))
+        self.step(tr, 0, False, "a", 0, unit=True)
+        self.step(tr, 1, False, "b", 1, unit=True)
+        tr.raw(f"s_add_u32 s{S_T}, s{S_T}, 2")
+        tr.raw("s_branch .Lw64_loop_%=")
+        tr.label(".Lw64_tail_%=")
+        tr.raw(f"s_add_u32 s{S_TMP}, s{S_T}, 1")
+        tr.raw(f"s_cmp_lt_u32 s{S_TMP}, %[n]")
+        tr.raw("s_cbranch_scc0 .Lw64_last0_%=")
+        self.step(tr, 0, False, "c", 0, unit=True)
+        self.step(tr, 1, True, "d", 1, unit=True)
+        tr.raw("s_branch .Lw64_done_%=")
+        tr.label(".Lw64_last0_%=")
+        # (the tracker goes on from step d's end: step e only adds distance
+        # on its own path before the epilogue, whose first reads of O wait
+        # out every MFMA result)
+        te = copy.deepcopy(tr)
+        n0 = len(te.out)
+        self.step(te, 0, True, "e", 0, unit=True)
+        tr.out.extend(te.out[n0:])
+        tr.label(".Lw64_done_%=")
+        self.epilogue(tr)
+        tr.raw("s_branch .Lxl_end_%=")
+        lines = tr.out
+        for blk in self.slow:
+            lines += blk
+        lines.append(".Lxl_end_%=:")
+        return lines
+
+    return dict(locals())
+
+
+for _name, _f in _xl_unit_methods().items():
+    setattr(Gen, _name, _f)
+
+
+def check_registers(lines, s_first=S_FIRST, s_last=S_LAST):
     """Every register named is inside the loop's ranges or an operand."""
     for ln in lines:
         for m in re.finditer(r"\b([va])\[(\d+):(\d+)\]|\b([va])(\d+)\b", ln):
@@ -707,13 +1086,38 @@ def check_registers(lines):
             else:
                 assert 0 <= lo and hi <= A_LAST, ln
         for m in re.finditer(r"\bs\[?(\d+)", ln):
-            assert S_FIRST <= int(m.group(1)) <= S_LAST + 3, ln
+            assert s_first <= int(m.group(1)) <= s_last + 3, ln
+
+
+def write_unit(path):
+    """kd_fa_xlong64_loop.inc: the unit block of fa_fwd_xlong64."""
+    out = ["// Generated by gen_w64_loop.py from this directory; do not edit.",
+           "// The per-unit block of fa_fwd_xlong64 (kd_fa_kernel.hip) as inline-asm text.", ""]
+    for T in ("bf16", "f16"):
+        lines = Gen(T).build_unit()
+        check_registers(lines, XL_S_FIRST, XL_S_LAST)
+        out.append(f"#define KD_XL64_UNIT_{T.upper()} \\")
+        for ln in lines:
+            out.append(f'    "{ln}\\n" \\')
+        out.append('    ""')
+        out.append("")
+    out.append("#define KD_XL64_CLOBBERS \\")
+    regs = [f'"v{i}"' for i in range(24, V_LAST + 1)] + [f'"a{i}"' for i in range(A_LAST + 1)] + \
+           [f'"s{i}"' for i in range(XL_S_FIRST, XL_S_LAST + 1)]
+    for k in range(0, len(regs), 16):
+        out.append("    " + ", ".join(regs[k:k + 16]) + ", \\")
+    out.append('    "vcc", "scc", "m0", "memory"')
+    with open(path, "w") as f:
+        f.write("\n".join(out) + "\n")
 
 
 def main(path=None, kpre=2, vpre=2, per1=4, check_at=29, check_spread=True):
+    """Writes the loop (path, default kd_fa_w64_loop.inc beside this file)
+    and the unit block (kd_fa_xlong64_loop.inc in the same directory)."""
     configure(kpre, vpre, per1, check_at, check_spread)
     here = os.path.dirname(os.path.abspath(__file__))
     path = path or os.path.join(here, "kd_fa_w64_loop.inc")
+    write_unit(os.path.join(os.path.dirname(os.path.abspath(path)), "kd_fa_xlong64_loop.inc"))
     out = ["// Generated by gen_w64_loop.py from this directory; do not edit.",
            "// The key loop of fa_fwd_w64 (kd_fa_kernel.hip) as inline-asm text.", ""]
     for T in ("bf16", "f16"):

@@ -296,6 +296,18 @@ static bool use_xlong(const kdfa::Args &a, int op, bool k_on_load, int route) {
     return (int64_t)(kdfa::kXlongRows - 1) * a.q_nb1 + 512 < ((int64_t)1 << 32);
 }
 
+// Of those, F32 Q (ops::attention's form) goes to the persistent kernel on
+// the 64-row loop when the 64-row kernel's limits hold too (the partial
+// last tile's weights, 31-bit K/V offsets) and a wave's 64 Q and O rows lie
+// within 31-bit offsets of its first row.  KD_FA_ROUTE_NO_XLONG64 keeps
+// them on fa_fwd_xlong (for comparisons).
+static bool use_xlong64(const kdfa::Args &a, int route) {
+    if ((route & KD_FA_ROUTE_NO_XLONG64) || a.q_type != KD_FA_TYPE_F32 || !w64_tail_ok(a)) return false;
+    const int64_t lim = (int64_t)1 << 31;
+    return (int64_t)(a.Lk - 1) * a.k_nb1 + 256 < lim && (int64_t)(a.Lk - 1) * a.v_nb1 + 256 < lim &&
+           63 * a.q_nb1 + 512 < lim && 63 * a.o_nb2 + 512 < lim;
+}
+
 // Query ranges per (b, h) for fa_fwd_xres: about one workgroup per CU
 // (256 on MI355X) in all, at least four 32-row blocks (one per wave) each.
 // (Two to four workgroups per CU, which would let the dispatcher balance
@@ -660,7 +672,7 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
     } else if (use_xlong(a, T, k_rope, route)) {
         a.n_qt = (int32_t)((Lq + kdfa::kXlongRows - 1) / kdfa::kXlongRows);
         a.n_blocks = (int32_t)(a.n_qt * H * B);
-        e = kdfa::launch_xlong(a, T, hs);
+        e = use_xlong64(a, route) ? kdfa::launch_xlong64(a, T, hs) : kdfa::launch_xlong(a, T, hs);
     } else if (use_w64(a, k_rope, route)) {
         a.n_qt = (int32_t)((Lq + kdfa::kW64Rows - 1) / kdfa::kW64Rows);
         a.n_blocks = (int32_t)(a.n_qt * H * B);

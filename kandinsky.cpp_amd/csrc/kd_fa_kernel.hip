@@ -2127,6 +2127,205 @@ static hipError_t launch_w64_t(const Args &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// fa_fwd_xlong64: the persistent long-prompt kernel on fa_fwd_w64's key loop,
+// for F32 Q (the text cross-attention as ops::attention hands it over:
+// src/core/ops.hpp:122-124, src/models/crossdit.hpp:198).
+//
+// One 4-wave workgroup per CU walks units of 256 query rows of one (b, h),
+// as fa_fwd_xlong does (XCD-contiguous unit ranges, workgroup j of an XCD
+// takes units j, j + w, ...).  Each unit runs one hand-scheduled block
+// (kd_fa_xlong64_loop.inc, written by gen_w64_loop.py): fa_fwd_w64's loop
+// with
+//   * the next unit's Q brought in during steps 0-4: each wave DMAs 128
+//     bytes of each of its 64 F32 rows per step into its raw area and, a step
+//     later, rounds them to the operand type into its Q fragment area, from
+//     which the next unit loads its fragments;
+//   * the next unit's K(0), K(1) fetched by the unit's last step and V(0)
+//     once every wave is done with the V buffers, before the O stores, so
+//     that the next unit waits for those three tiles but not for the stores
+//     (loads and stores complete in issue order);
+//   * the O epilogue in the block: O / l staged per 32 rows in the raw area
+//     and stored as whole 128-byte lines through a buffer resource that ends
+//     at the last valid row (rows past Lq are not written).
+// Per row the arithmetic is fa_fwd_w64's (and so fa_fwd_d128's): the
+// results are bitwise equal.
+//
+// LDS: K and V tiles 2 x 2 x 16 KiB, per wave 16 KiB of Q fragments (64 ..
+// 128 KiB) and 8 KiB of raw Q pieces / O staging (128 .. 160 KiB).
+// ---------------------------------------------------------------------------
+#include "kd_fa_xlong64_loop.inc"
+
+constexpr int kX64QOff = 65536;
+constexpr int kX64RawOff = 131072;
+constexpr int kX64Raw = 8192;
+constexpr int kX64Lds = 163840;
+static_assert(kX64RawOff + 4 * kX64Raw == kX64Lds, "LDS plan");
+
+template <typename T>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void fa_fwd_xlong64(Args a) {
+    typedef Elem<T> E;
+    typedef typename E::vec8 vec8;
+    __shared__ __attribute__((aligned(1024))) char lds_arr[kX64Lds];
+    lds_t *const lds = LDS_PTR(char, lds_arr);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31;
+    const int hi = lane >> 5;
+
+    // this workgroup's units: j, j + wpx, ... within its XCD's range
+    const int n_units = a.n_blocks;
+    const int wpx = (int)(gridDim.x >> 3);
+    const int per = (n_units + 7) >> 3;
+    const int xcd = (int)(blockIdx.x & 7);
+    const int u_end = min((xcd + 1) * per, n_units);
+    int u = xcd * per + (int)(blockIdx.x >> 3);
+    if (u >= u_end) return;   // before any barrier
+
+    // the first unit's Q fragments -> LDS (load_q_frags: rounding and sign)
+    {
+        const int qt = u % a.n_qt, bh = u / a.n_qt;
+        const int h = bh % a.H, b = bh / a.H;
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            const int q_row = qt * 256 + wave * 64 + qb * 32 + l32;
+            const int q_ld = q_row < a.Lq ? q_row : a.Lq - 1;
+            vec8 qf[8];
+            load_q_frags<T, KD_FA_ROPE_NONE, true>(a, q_ld, h, b, hi, qf);
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks)
+                *reinterpret_cast<__attribute__((address_space(3))) vec8 *>(
+                    lds + kX64QOff + wave * 16384 + (qb * 8 + ks) * 1024 + lane * 16) = qf[ks];
+        }
+    }
+
+    // per-lane LDS offsets of the operand reads and the K/V DMA (fa_fwd_w64's)
+    uint32_t krd[8], vrd[4];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) krd[ks] = lds0 + l32 * 256 + (((2 * ks + hi) ^ (lane & 15)) << 4);
+    const int v_sub = (lane & 15) >> 2;
+    const int v_c_lo = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+#pragma unroll
+    for (int dblk = 0; dblk < 4; ++dblk)
+        vrd[dblk] = lds0 + 2048 * hi + 256 * v_sub + (((4 * dblk + v_c_lo) ^ v_swz(v_sub)) << 4) + 8 * (lane & 1);
+    const int r0 = 4 * wave + (lane >> 4);
+    const int pc = lane & 15;
+    uint32_t kdma[4], vdma[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        kdma[j] = (uint32_t)(k_row_of(r0) + 16 * j) * (uint32_t)a.k_nb1 + ((pc ^ (r0 & 15)) << 4);
+        vdma[j] = (uint32_t)(r0 + 16 * j) * (uint32_t)a.v_nb1 + ((pc ^ v_swz(r0)) << 4);
+    }
+    const uint32_t qrd = lds0 + kX64QOff + wave * 16384 + lane * 16;
+    const uint32_t dmab = __builtin_amdgcn_readfirstlane(lds0 + wave * 1024);
+    const uint32_t rawb = __builtin_amdgcn_readfirstlane(lds0 + kX64RawOff + wave * kX64Raw);
+    const uint32_t rawdelta = __builtin_amdgcn_readfirstlane((uint32_t)(kX64RawOff - kX64QOff) - wave * 8192u);
+    // the next unit's Q rows: lane l reads row 32 qb + l % 32 of its wave
+    const uint32_t qoff0 = (uint32_t)l32 * (uint32_t)a.q_nb1 + 32u * (uint32_t)hi;
+    const uint32_t qoff1 = qoff0 + 32u * (uint32_t)a.q_nb1;
+
+    const uint32_t rw3 = 0x00020000u;
+    const uint32_t kw2 = __builtin_amdgcn_readfirstlane((uint32_t)(a.Lk - 1) * (uint32_t)a.k_nb1 + 256u);
+    const uint32_t vw2 = __builtin_amdgcn_readfirstlane((uint32_t)(a.Lk - 1) * (uint32_t)a.v_nb1 + 256u);
+    const uint32_t ktile = __builtin_amdgcn_readfirstlane(64u * (uint32_t)a.k_nb1);
+    const uint32_t vtile = __builtin_amdgcn_readfirstlane(64u * (uint32_t)a.v_nb1);
+    const uint32_t n_tiles = __builtin_amdgcn_readfirstlane((uint32_t)((a.Lk + kBN - 1) / kBN));
+    const int rem = a.Lk - kBN * ((int)n_tiles - 1);
+    const uint32_t mstep = __builtin_amdgcn_readfirstlane(rem < kBN ? n_tiles - 2 : 0xffffffffu);
+    const int thr = rem - 8 * hi;
+    const float c2 = __builtin_fabsf(a.scale_log2);
+    const uint32_t qsgn = a.scale_log2 < 0.0f ? 0x80008000u : 0u;
+    const uint32_t ot = a.o_type == KD_FA_TYPE_F32 ? 0u : a.o_type == KD_FA_TYPE_BF16 ? 1u : 2u;
+    const uint32_t orow_bytes = ot == 0 ? 512u : 256u;
+    const uint32_t onb2 = (uint32_t)a.o_nb2;
+    const uint32_t o8 = 8u * onb2;
+
+    // buffer resource words of a unit's K, V (from its (b, h)), Q and O
+    // (from this wave's first row; the record count ends at the last valid
+    // row, 0 when none is)
+    auto res_lo = [](const char *p) { return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p); };
+    auto res_hi = [](const char *p) {
+        return __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)(uintptr_t)p >> 32) & 0xffffu);
+    };
+    uint32_t first = 1;
+    for (;;) {
+        const int nu = u + wpx;
+        const bool has_next = nu < u_end;
+        const int qt = u % a.n_qt, bh = u / a.n_qt;
+        const int h = bh % a.H, b = bh / a.H;
+        const char *kb = a.k + (int64_t)(h / a.rk2) * a.k_nb2 + (int64_t)(b / a.rk3) * a.k_nb3;
+        const char *vb = a.v + (int64_t)(h / a.rv2) * a.v_nb2 + (int64_t)(b / a.rv3) * a.v_nb3;
+        const int orow = qt * 256 + wave * 64;
+        const char *ob = a.o + (int64_t)b * a.o_nb3 + (int64_t)h * a.o_nb1 + (int64_t)orow * a.o_nb2;
+        const int o_valid = min(a.Lq - orow, 64);
+        const uint32_t ow2 = o_valid > 0 ? (uint32_t)(o_valid - 1) * onb2 + orow_bytes : 0u;
+        const char *nkb = kb, *nvb = vb, *nqb = a.q;
+        uint32_t nkw2 = 0, nvw2 = 0, nqw2 = 0;
+        if (has_next) {
+            const int nqt = nu % a.n_qt, nbh = nu / a.n_qt;
+            const int nh = nbh % a.H, nb = nbh / a.H;
+            nkb = a.k + (int64_t)(nh / a.rk2) * a.k_nb2 + (int64_t)(nb / a.rk3) * a.k_nb3;
+            nvb = a.v + (int64_t)(nh / a.rv2) * a.v_nb2 + (int64_t)(nb / a.rv3) * a.v_nb3;
+            const int qrow = nqt * 256 + wave * 64;
+            nqb = a.q + (int64_t)nh * a.q_nb2 + (int64_t)nb * a.q_nb3 + (int64_t)qrow * a.q_nb1;
+            const int q_valid = min(a.Lq - qrow, 64);
+            nkw2 = kw2;
+            nvw2 = vw2;
+            nqw2 = q_valid > 0 ? (uint32_t)(q_valid - 1) * (uint32_t)a.q_nb1 + 512u : 0u;
+        }
+        const uint32_t kw0 = res_lo(kb), kw1 = res_hi(kb), vw0 = res_lo(vb), vw1 = res_hi(vb);
+        const uint32_t ow0 = res_lo(ob), ow1 = res_hi(ob);
+        const uint32_t nkw0 = res_lo(nkb), nkw1 = res_hi(nkb), nvw0 = res_lo(nvb), nvw1 = res_hi(nvb);
+        const uint32_t nqw0 = res_lo(nqb), nqw1 = res_hi(nqb);
+        const uint32_t ow2u = __builtin_amdgcn_readfirstlane(ow2);
+        const uint32_t nkw2u = __builtin_amdgcn_readfirstlane(nkw2), nvw2u = __builtin_amdgcn_readfirstlane(nvw2);
+        const uint32_t nqw2u = __builtin_amdgcn_readfirstlane(nqw2);
+#define KD_XL64_OPERANDS                                                                                      \
+    [krd0] "v"(krd[0]), [krd1] "v"(krd[1]), [krd2] "v"(krd[2]), [krd3] "v"(krd[3]), [krd4] "v"(krd[4]),       \
+        [krd5] "v"(krd[5]), [krd6] "v"(krd[6]), [krd7] "v"(krd[7]), [vrd0] "v"(vrd[0]), [vrd1] "v"(vrd[1]),   \
+        [vrd2] "v"(vrd[2]), [vrd3] "v"(vrd[3]), [kdma0] "v"(kdma[0]), [kdma1] "v"(kdma[1]),                  \
+        [kdma2] "v"(kdma[2]), [kdma3] "v"(kdma[3]), [vdma0] "v"(vdma[0]), [vdma1] "v"(vdma[1]),              \
+        [vdma2] "v"(vdma[2]), [vdma3] "v"(vdma[3]), [qrd] "v"(qrd), [thr] "v"(thr), [qoff0] "v"(qoff0),     \
+        [qoff1] "v"(qoff1), [kw0] "s"(kw0), [kw1] "s"(kw1), [kw2] "s"(kw2), [rw3] "s"(rw3), [vw0] "s"(vw0),   \
+        [vw1] "s"(vw1), [vw2] "s"(vw2), [ktile] "s"(ktile), [vtile] "s"(vtile), [n] "s"(n_tiles),            \
+        [c2] "s"(c2), [dmab] "s"(dmab), [mstep] "s"(mstep), [first] "s"(first), [nkw0] "s"(nkw0),            \
+        [nkw1] "s"(nkw1), [nkw2] "s"(nkw2u), [nvw0] "s"(nvw0), [nvw1] "s"(nvw1), [nvw2] "s"(nvw2u),           \
+        [nqw0] "s"(nqw0), [nqw1] "s"(nqw1), [nqw2] "s"(nqw2u), [ow0] "s"(ow0), [ow1] "s"(ow1),               \
+        [ow2] "s"(ow2u), [o8] "s"(o8), [onb2] "s"(onb2), [ot] "s"(ot), [qsgn] "s"(qsgn), [rawb] "s"(rawb),     \
+        [rawdelta] "s"(rawdelta)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+        if constexpr (__is_same(T, __bf16))
+            asm volatile(KD_XL64_UNIT_BF16 : : KD_XL64_OPERANDS : KD_XL64_CLOBBERS);
+        else
+            asm volatile(KD_XL64_UNIT_F16 : : KD_XL64_OPERANDS : KD_XL64_CLOBBERS);
+#pragma clang diagnostic pop
+#undef KD_XL64_OPERANDS
+        if (!has_next) break;
+        u = nu;
+        first = 0;
+    }
+}
+
+template <typename T>
+static void launch_xlong64_t(const Args &a, hipStream_t s) {
+    // at most one workgroup per CU (256), a multiple of the 8 XCDs
+    const int g = a.n_blocks < 256 ? (a.n_blocks + 7) / 8 * 8 : 256;
+    hipLaunchKernelGGL((fa_fwd_xlong64<T>), dim3(g), dim3(256), 0, s, a);
+}
+
+hipError_t launch_xlong64(const Args &a, int kv_type, hipStream_t s) {
+    if (kv_type == KD_FA_TYPE_BF16)
+        launch_xlong64_t<__bf16>(a, s);
+    else
+        launch_xlong64_t<_Float16>(a, s);
+    return hipGetLastError();
+}
+
 template <typename T>
 static void launch_xres_t(const Args &a, hipStream_t s) {
     const dim3 g(a.n_blocks), b(64 * kXWaves);

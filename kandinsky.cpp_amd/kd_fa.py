@@ -64,6 +64,7 @@ ROUTE_W64_SHORT = 16
 ROUTE_STAGED = 32
 ROUTE_SUMMARY = 64
 ROUTE_NO_XLONG = 128
+ROUTE_NO_XLONG64 = 256
 
 
 class KdFaTensor(ctypes.Structure):

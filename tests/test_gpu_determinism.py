@@ -9,7 +9,8 @@ choice of kd_fa_run / kd_fa_run_ws / kd_fa_rope_run / kd_fa_dit_run takes:
 the 64-row kernel, the 32-row kernel (pipelined unmasked loop with 4- and
 8-wave workgroups, masked loop, K rotated on load), the short-key kernel
 (masked, unmasked, F32 Q, with the mask summary), the persistent
-long-prompt kernel (F32 and 16-bit Q), the staged schedule, the
+long-prompt kernels (the 64-row one for F32 Q; the 32-row one for F32 and
+16-bit Q), the staged schedule, the
 F32 cast pre-pass, and the D = 512 kernel with and without its key split.
 """
 import pytest
@@ -62,7 +63,8 @@ PLAIN = [
     ("xres_masked", 256, True, kd_fa.ROUTE_DEFAULT, torch.bfloat16, torch.bfloat16),
     ("xres_unmasked_q32", 77, False, kd_fa.ROUTE_DEFAULT, torch.float16, torch.float32),
     ("d128_short_masked", 200, True, kd_fa.ROUTE_NO_XRES, torch.float16, torch.float16),
-    ("xlong_f16_q32", 512, False, kd_fa.ROUTE_DEFAULT, torch.float16, torch.float32),
+    ("xlong64_f16_q32", 512, False, kd_fa.ROUTE_DEFAULT, torch.float16, torch.float32),
+    ("xlong_f16_q32", 512, False, kd_fa.ROUTE_NO_XLONG64, torch.float16, torch.float32),
     ("xlong_bf16_tail", 300, False, kd_fa.ROUTE_DEFAULT, torch.bfloat16, torch.bfloat16),
 ]
 

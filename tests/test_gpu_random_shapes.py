@@ -6,8 +6,9 @@ K's type), a mask (none, a per-batch padding mask, or random finite values
 with -inf holes), and a scale (positive or negative), then runs the node
 under each routing choice of kd_fa_set_routing: as routed, with the 64-row
 and long-prompt kernels out, with the short-key kernel out, with the 64-row
-kernel taking the short unmasked key sets too, and with all specialised
-kernels out.  Every
+kernel taking the short unmasked key sets too, with all specialised
+kernels out, and with the persistent 32-row long-prompt kernel in place of
+the 64-row one.  Every
 kernel computes each query row with the same arithmetic, so all outputs must
 be bitwise equal; the routed one must also match the float64 oracle on every
 row.  Odd seeds give the mask rows whole 8-key chunks (ggml pads them; the
@@ -28,7 +29,7 @@ pytestmark = pytest.mark.gpu
 
 DEV = "cuda:0"
 ROUTES = [kd_fa.ROUTE_DEFAULT, kd_fa.ROUTE_NO_W64, kd_fa.ROUTE_NO_XRES, kd_fa.ROUTE_W64_SHORT,
-          kd_fa.ROUTE_NO_W64 | kd_fa.ROUTE_NO_XRES]
+          kd_fa.ROUTE_NO_W64 | kd_fa.ROUTE_NO_XRES, kd_fa.ROUTE_NO_XLONG64]
 
 
 def _need_gpu():

@@ -1,14 +1,16 @@
-"""GPU checks of the persistent long-prompt kernel (fa_fwd_xlong), which
-takes the unmasked calls with 257-1,024 keys whose K is read as stored and
-whose Q is neither rotated nor normalised -- the text cross-attention of a
-long prompt (src/models/crossdit.hpp:198, no mask; up to 512 prompt tokens,
-src/models/qwen_tokenizer.hpp:128,183-186).
+"""GPU checks of the persistent long-prompt kernels, which take the unmasked
+calls with 257-1,024 keys whose K is read as stored and whose Q is neither
+rotated nor normalised -- the text cross-attention of a long prompt
+(src/models/crossdit.hpp:198, no mask; up to 512 prompt tokens,
+src/models/qwen_tokenizer.hpp:128,183-186): fa_fwd_xlong64 (F32 Q, the
+64-row loop) and fa_fwd_xlong (16-bit Q, and F32 Q with scale 0 and a
+partial last tile).
 
-Each case runs twice through the C ABI: once as routed (fa_fwd_xlong) and
-once with the kernel routed out (kd_fa_set_routing: the 32-row kernel,
-fa_fwd_d128); the outputs must be bitwise equal, since both kernels perform
-the same arithmetic per query row.  Parity against the float64 oracle
-completes each case.  The shapes walk the kernel's structure: 5 to 16 key
+Each case runs through the C ABI as routed and with the kernels routed out
+(kd_fa_set_routing): KD_FA_ROUTE_NO_XLONG64 (fa_fwd_xlong) and
+KD_FA_ROUTE_NO_XLONG (the 32-row kernel, fa_fwd_d128); the outputs must be
+bitwise equal, since the kernels perform the same arithmetic per query row.
+Parity against the float64 oracle completes each case.  The shapes walk the kernel's structure: 5 to 16 key
 tiles (an odd or even count, with or without a partial last tile: Lk = 257,
 300, 320, 448, 512, 513, 640, 896, 1,000, 1,024), Q in F32 (four 128-byte pieces per row
 brought in during a unit's first steps) or in K's type (two), workgroups
@@ -42,12 +44,17 @@ def _announce(msg):
 
 
 def _both(fn):
-    """(routed output, 32-row kernel output) of fn()."""
+    """(routed output, 32-row kernel output) of fn(); the persistent 32-row
+    kernel's output (KD_FA_ROUTE_NO_XLONG64) must equal the routed one."""
     with kd_fa.routing(kd_fa.ROUTE_NO_XLONG):
         ref = fn()
         torch.cuda.synchronize()
+    with kd_fa.routing(kd_fa.ROUTE_NO_XLONG64):
+        mid = fn()
+        torch.cuda.synchronize()
     out = fn()
     torch.cuda.synchronize()
+    assert torch.equal(out, mid)
     return out, ref
 
 
