@@ -378,10 +378,12 @@ enum {
                                    shape allows, also where one on-load launch is cheaper */
     KD_FA_ROUTE_SUMMARY = 64,   /* mask summary for every masked short-key node with the
                                    workspace, also below 65,536 query rows             */
-    KD_FA_ROUTE_NO_XLONG = 128, /* unmasked key sets of 257-1,024 keys: the 32-row
-                                   kernel, not the persistent long-prompt ones         */
-    KD_FA_ROUTE_NO_XLONG64 = 256 /* those key sets with F32 Q: the persistent 32-row
-                                   kernel, not the persistent 64-row one               */
+    KD_FA_ROUTE_NO_XLONG = 128, /* unmasked key sets of more than 256 keys: not the
+                                   persistent kernels (the 32-row kernel up to 896
+                                   keys, the 64-row one above)                         */
+    KD_FA_ROUTE_NO_XLONG64 = 256 /* those with F32 Q: not the persistent 64-row kernel
+                                   (the persistent 32-row one up to 1,024 keys, the
+                                   64-row one above)                                   */
 };
 int kd_fa_set_routing(int flags);
 

@@ -251,14 +251,14 @@ static bool w64_tail_ok(const kdfa::Args &a) { return a.Lk % 64 == 0 || a.scale_
 
 // The 64-rows-per-wave kernel takes the unmasked calls whose K streams from
 // memory as stored (no transform on load) and that have more than
-// kShortKeys keys and that the long-prompt kernel does not take (use_xlong
-// is asked first); its buffer-resource offsets are 32-bit.  (With one
+// kShortKeys keys and that the persistent kernels do not take (use_xlong64
+// and use_xlong are asked first); its buffer-resource offsets are 32-bit.  (With one
 // workgroup per CU, all CUs load Q, run the few key steps of a short key set
 // and store O in step, while the 32-row kernel's 4-wave workgroups, two per
 // CU, overlap one's memory phases with the other's key loop: cross-attention
 // with Q F32 [128, 31744, 32, 2] and 320 keys 0.62 against 0.72 ms, 512
 // keys 0.78 against 0.85, 896 keys 1.14 against 1.15, 1,024 keys even --
-// the range where the persistent long-prompt kernel now runs when it can.)
+// the range where the persistent kernels now run when they can.)
 // For comparisons, KD_FA_ROUTE_NO_W64 routes every call to the 32-row
 // kernel and KD_FA_ROUTE_W64_SHORT the short key sets too to this one.
 static bool use_w64(const kdfa::Args &a, bool k_on_load, int route) {
@@ -281,31 +281,43 @@ static bool use_xres(const kdfa::Args &a, int op, const kd_fa_desc *d, bool k_on
     return true;
 }
 
-// Unmasked key sets just past the LDS-resident kernel's (the text
-// cross-attention of a long prompt) go to the persistent kernel that streams
-// K and V with the next query tile's Q loaded during the key loop, when K is
-// read as stored, Q is neither rotated nor normalised and is stored as F32
-// or in K's type, and a unit's Q rows lie within 32-bit offsets of its first
-// row.  KD_FA_ROUTE_NO_XLONG and KD_FA_ROUTE_NO_W64 route them to the 32-row
-// kernel, KD_FA_ROUTE_W64_SHORT to the 64-row one (for comparisons).
+// Unmasked key sets past the LDS-resident kernel's with F32 Q (the node as
+// ops::attention hands it over: the text cross-attention of a long prompt,
+// and any longer unmasked node) go to the persistent kernel on the 64-row
+// loop, fa_fwd_xlong64, when K is read as stored, Q is neither rotated nor
+// normalised, the 64-row kernel's limits hold (the partial last tile's
+// weights, 31-bit K/V offsets) and a wave's 64 Q and O rows lie within
+// 31-bit offsets of its first row.  (It beats fa_fwd_w64, whose workgroups
+// load Q, run the key loop and store O in sequence, at every length
+// measured: 1,024 keys 1.14 against 1.24 ms, 2,048 keys 1.99 against 2.07,
+// 8,192 keys 7.14 against 7.16, Q F32 [128, 31744, 32, 2].)
+// KD_FA_ROUTE_NO_XLONG64 routes them as if it did not exist,
+// KD_FA_ROUTE_NO_XLONG, KD_FA_ROUTE_NO_W64 and KD_FA_ROUTE_W64_SHORT keep
+// them off the persistent kernels (for comparisons).
+static bool use_xlong64(const kdfa::Args &a, bool k_on_load, int route) {
+    if (route & (KD_FA_ROUTE_NO_XLONG | KD_FA_ROUTE_NO_XLONG64 | KD_FA_ROUTE_NO_W64 | KD_FA_ROUTE_W64_SHORT))
+        return false;
+    if (a.m || k_on_load || a.rope_mode != KD_FA_ROPE_NONE || a.qn_w) return false;
+    if (a.Lk <= kdfa::kXresMaxKeys || a.q_type != KD_FA_TYPE_F32 || !w64_tail_ok(a)) return false;
+    const int64_t lim = (int64_t)1 << 31;
+    return (int64_t)(a.Lk - 1) * a.k_nb1 + 256 < lim && (int64_t)(a.Lk - 1) * a.v_nb1 + 256 < lim &&
+           63 * a.q_nb1 + 512 < lim && 63 * a.o_nb2 + 512 < lim;
+}
+
+// The other unmasked key sets just past the LDS-resident kernel's (Q in K's
+// type, or F32 with scale 0 and a partial last tile) go to the persistent
+// kernel that streams K and V with the next query tile's Q loaded during the
+// key loop, fa_fwd_xlong, when K is read as stored, Q is neither rotated nor
+// normalised and is stored as F32 or in K's type, and a unit's Q rows lie
+// within 32-bit offsets of its first row.  KD_FA_ROUTE_NO_XLONG and
+// KD_FA_ROUTE_NO_W64 route them to the 32-row kernel, KD_FA_ROUTE_W64_SHORT
+// to the 64-row one (for comparisons).
 static bool use_xlong(const kdfa::Args &a, int op, bool k_on_load, int route) {
     if (route & (KD_FA_ROUTE_NO_XLONG | KD_FA_ROUTE_NO_W64 | KD_FA_ROUTE_W64_SHORT)) return false;
     if (a.m || k_on_load || a.rope_mode != KD_FA_ROPE_NONE || a.qn_w) return false;
     if (a.Lk <= kdfa::kXresMaxKeys || a.Lk > kdfa::kXlongMaxKeys) return false;
     if (a.q_type != KD_FA_TYPE_F32 && a.q_type != op) return false;
     return (int64_t)(kdfa::kXlongRows - 1) * a.q_nb1 + 512 < ((int64_t)1 << 32);
-}
-
-// Of those, F32 Q (ops::attention's form) goes to the persistent kernel on
-// the 64-row loop when the 64-row kernel's limits hold too (the partial
-// last tile's weights, 31-bit K/V offsets) and a wave's 64 Q and O rows lie
-// within 31-bit offsets of its first row.  KD_FA_ROUTE_NO_XLONG64 keeps
-// them on fa_fwd_xlong (for comparisons).
-static bool use_xlong64(const kdfa::Args &a, int route) {
-    if ((route & KD_FA_ROUTE_NO_XLONG64) || a.q_type != KD_FA_TYPE_F32 || !w64_tail_ok(a)) return false;
-    const int64_t lim = (int64_t)1 << 31;
-    return (int64_t)(a.Lk - 1) * a.k_nb1 + 256 < lim && (int64_t)(a.Lk - 1) * a.v_nb1 + 256 < lim &&
-           63 * a.q_nb1 + 512 < lim && 63 * a.o_nb2 + 512 < lim;
 }
 
 // Query ranges per (b, h) for fa_fwd_xres: about one workgroup per CU
@@ -669,10 +681,14 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
             a.m_live_nqb = (int32_t)((Lq + 31) / 32);
         }
         e = kdfa::launch_xres(a, T, hs);
+    } else if (use_xlong64(a, k_rope, route)) {
+        a.n_qt = (int32_t)((Lq + kdfa::kXlongRows - 1) / kdfa::kXlongRows);
+        a.n_blocks = (int32_t)(a.n_qt * H * B);
+        e = kdfa::launch_xlong64(a, T, hs);
     } else if (use_xlong(a, T, k_rope, route)) {
         a.n_qt = (int32_t)((Lq + kdfa::kXlongRows - 1) / kdfa::kXlongRows);
         a.n_blocks = (int32_t)(a.n_qt * H * B);
-        e = use_xlong64(a, route) ? kdfa::launch_xlong64(a, T, hs) : kdfa::launch_xlong(a, T, hs);
+        e = kdfa::launch_xlong(a, T, hs);
     } else if (use_w64(a, k_rope, route)) {
         a.n_qt = (int32_t)((Lq + kdfa::kW64Rows - 1) / kdfa::kW64Rows);
         a.n_blocks = (int32_t)(a.n_qt * H * B);

@@ -108,9 +108,10 @@ hipError_t launch_xres(const Args &a, int kv_type, hipStream_t stream);
 constexpr int kXlongRows = 256;
 constexpr int kXlongMaxKeys = 1024;
 hipError_t launch_xlong(const Args &a, int kv_type, hipStream_t stream);
-// The same key sets with F32 Q on fa_fwd_w64's key loop (fa_fwd_xlong64):
-// units of kXlongRows rows as above; a unit's Q and O rows (64 per wave)
-// within 31-bit offsets of the wave's first row, K and V as fa_fwd_w64's.
+// Unmasked key sets of more than kXresMaxKeys keys (any number) with F32 Q
+// on fa_fwd_w64's key loop (fa_fwd_xlong64): units of kXlongRows rows as
+// above; a wave's Q and O rows (64) within 31-bit offsets of its first row,
+// K and V as fa_fwd_w64's.
 hipError_t launch_xlong64(const Args &a, int kv_type, hipStream_t stream);
 
 // Enqueue the mask summary fa_fwd_xres reads through a.m_live: one 32-bit

@@ -1,15 +1,16 @@
 """GPU checks of the persistent long-prompt kernels, which take the unmasked
-calls with 257-1,024 keys whose K is read as stored and whose Q is neither
-rotated nor normalised -- the text cross-attention of a long prompt
+calls with more than 256 keys whose K is read as stored and whose Q is
+neither rotated nor normalised -- the text cross-attention of a long prompt
 (src/models/crossdit.hpp:198, no mask; up to 512 prompt tokens,
 src/models/qwen_tokenizer.hpp:128,183-186): fa_fwd_xlong64 (F32 Q, the
-64-row loop) and fa_fwd_xlong (16-bit Q, and F32 Q with scale 0 and a
-partial last tile).
+64-row loop, any number of keys) and fa_fwd_xlong (up to 1,024 keys: 16-bit
+Q, and F32 Q with scale 0 and a partial last tile).
 
 Each case runs through the C ABI as routed and with the kernels routed out
-(kd_fa_set_routing): KD_FA_ROUTE_NO_XLONG64 (fa_fwd_xlong) and
-KD_FA_ROUTE_NO_XLONG (the 32-row kernel, fa_fwd_d128); the outputs must be
-bitwise equal, since the kernels perform the same arithmetic per query row.
+(kd_fa_set_routing): KD_FA_ROUTE_NO_XLONG64 (fa_fwd_xlong, or fa_fwd_w64
+past 1,024 keys) and KD_FA_ROUTE_NO_XLONG (the 32-row kernel fa_fwd_d128, or
+fa_fwd_w64 past 896 keys); the outputs must be bitwise equal, since the
+kernels perform the same arithmetic per query row.
 Parity against the float64 oracle completes each case.  The shapes walk the kernel's structure: 5 to 16 key
 tiles (an odd or even count, with or without a partial last tile: Lk = 257,
 300, 320, 448, 512, 513, 640, 896, 1,000, 1,024), Q in F32 (four 128-byte pieces per row
@@ -68,10 +69,12 @@ CASES = [
     (1, 2, 2, 1, 300, 513, torch.bfloat16, torch.float32),     # 9 tiles, one key in the last
     (1, 4, 4, 1, 5000, 896, torch.bfloat16, torch.float32),    # 14 tiles
     (1, 2, 2, 1, 1200, 1000, torch.float16, torch.float32),    # 16 tiles, the last partial
-    (1, 2, 2, 1, 900, 1024, torch.bfloat16, torch.bfloat16),   # 16 tiles, the largest key set
+    (1, 2, 2, 1, 900, 1024, torch.bfloat16, torch.bfloat16),   # 16 tiles, fa_fwd_xlong's largest key set
     (1, 1, 1, 1, 100, 640, torch.float16, torch.float32),      # one unit in all
     (1, 5, 5, 1, 3000, 384, torch.float16, torch.float16),     # 60 units: XCD ranges of 8, the last short
     (1, 2, 1, 1, 20, 600, torch.bfloat16, torch.float32),      # fewer rows than one wave's 32
+    (1, 2, 2, 1, 700, 1500, torch.float16, torch.float32),     # past 1,024 keys: F32 Q only
+    (2, 2, 1, 1, 333, 2113, torch.bfloat16, torch.float32),    # 34 tiles, GQA
 ]
 
 
