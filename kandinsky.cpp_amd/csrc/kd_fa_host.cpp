@@ -885,7 +885,7 @@ const char *kd_fa_strerror(int status) {
     }
 }
 
-int kd_fa_version(void) { return 301; }
+int kd_fa_version(void) { return 302; }
 
 int kd_fa_abi_version(void) { return KD_FA_ABI_VERSION; }
 
