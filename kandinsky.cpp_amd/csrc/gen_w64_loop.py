@@ -719,6 +719,7 @@ XL_RAW_W = 8192
 XL_PIECES = 4          # 128-byte pieces of an F32 row, one per step in steps 0-3
 XL_PIECE_DMAS = 8      # DMA instructions per piece and wave
 XL_KV_DMAS = 8         # K/V DMA instructions per step and wave (the last step: K(0), K(1) of the next unit)
+XL_Q16_DMAS = 4        # Q in the operand type: fragment DMAs per step and wave (steps 0-3)
 XL_PITCH = 144         # O staging: bytes per row (128 + 16: no bank conflicts)
 S_NQ = 80              # s[80:83] the next unit's Q buffer resource
 S_T2, S_T3 = 96, 97    # temporaries of the unit block
@@ -766,7 +767,7 @@ def _xl_unit_methods():
         self.piece_index(tr, toff)
         tr.raw(f"s_cmp_lt_u32 s{S_T2}, {XL_PIECES}")
         tr.raw(f"s_cbranch_scc0 {w0}")
-        tr.raw(f"s_waitcnt vmcnt({XL_PIECE_DMAS})")
+        tr.raw(f"s_waitcnt vmcnt({XL_Q16_DMAS if self.q16 else XL_PIECE_DMAS})")
         tr.raw(f"s_branch {wd}")
         tr.label(w0)
         tr.raw("s_waitcnt vmcnt(0)")
@@ -785,6 +786,9 @@ def _xl_unit_methods():
         tracker may go on as on the path that skips it."""
         R = S_BASE[p]
         skip, noconv = f".Lxl_nopiece_{tag}_%=", f".Lxl_noconv_{tag}_%="
+        if self.q16:
+            self.piece_block_q16(tr, R, toff, tag)
+            return
         self.piece_index(tr, toff)
         tr.raw(f"s_cmp_gt_u32 s{S_T2}, {XL_PIECES}")
         tr.raw(f"s_cbranch_scc1 {skip}")
@@ -826,6 +830,31 @@ def _xl_unit_methods():
                     tr.raw(f"s_add_u32 m0, %[rawb], {1024 * i}")
                     tr.raw("s_nop 0")
                     tr.raw(f"buffer_load_dwordx4 {vr(R + 52 + i)}, s[{S_NQ}:{S_NQ + 3}], 0 offen lds")
+        tr.label(skip)
+
+    def piece_block_q16(self, tr, R, toff, tag):
+        """Q stored in the operand type: in step t <= 3 each wave DMAs the
+        fragments of k-steps 2 t and 2 t + 1 of its 64 rows straight into
+        the fragment area (the fragment layout is the rows' 16-byte chunks:
+        lane l of fragment (qb, ks) holds row 32 qb + l % 32, bytes
+        32 ks + 16 (l / 32)); nothing to convert.  Their DMAs stay in flight
+        past the step's end (step_wait); the next unit's first wait, for the
+        tiles issued after them, covers them."""
+        skip = f".Lxl_nopiece_{tag}_%="
+        self.piece_index(tr, toff)
+        tr.raw(f"s_cmp_ge_u32 s{S_T2}, {XL_PIECES}")
+        tr.raw(f"s_cbranch_scc1 {skip}")
+        tr.raw(f"s_lshl_b32 s{S_T2}, s{S_T2}, 6")
+        tr.raw(f"s_lshl_b32 s{S_T3}, s{S_T2}, 5")
+        for qb in range(2):
+            for kk in range(2):
+                i = 2 * qb + kk
+                tr.raw(f"s_add_u32 s{S_VCC}, s{S_T2}, {32 * kk}")
+                tr.raw(f"v_add_u32 {vr(R + 52 + i)}, s{S_VCC}, %[qoff{qb}]")
+                tr.raw(f"s_add_u32 m0, %[qfb], s{S_T3}")
+                tr.raw(f"s_add_u32 m0, m0, {1024 * (8 * qb + kk)}")
+                tr.raw("s_nop 0")
+                tr.raw(f"buffer_load_dwordx4 {vr(R + 52 + i)}, s[{S_NQ}:{S_NQ + 3}], 0 offen lds")
         tr.label(skip)
 
     def epilogue(self, tr):
@@ -969,13 +998,14 @@ def _xl_unit_methods():
                 e(Ins(f"buffer_store_dwordx4 {vrng(rb + 4 * jr, 4)}, {vr(EP_OROW[4 * qb + jr])}, s[{S_K}:{S_K + 3}], "
                       f"0 offen offset:{128 * dp} nt", "vmem", vset(rb + 4 * jr, 4) | {vr(EP_OROW[4 * qb + jr])}, ()))
 
-    def build_unit(self):
+    def build_unit(self, q16=False):
         """The unit block of fa_fwd_xlong64: the loop of build() for one
         unit, whose Q fragments are in the fragment area; the first unit of
         a workgroup (operand first != 0) fetches its own K(0), V(0), K(1),
         later ones find them issued by the previous unit and wait only for
         those (the previous unit's O stores, issued after them, complete in
         issue order)."""
+        self.q16 = q16
         tr = Tracker()
         e = tr.emit
         for qb in range(2):
@@ -983,8 +1013,12 @@ def _xl_unit_methods():
             e(valu(f"v_mov_b32 {vr(LH[qb])}, 0", (), {vr(LH[qb])}))
         for i in range(128):
             e(Ins(f"v_accvgpr_write_b32 a{A_O + i}, 0", "accw", (), {f"a{A_O + i}"}))
-        for i in range(16):
-            e(Ins(f"ds_read_b128 {arng(A_Q + 4 * i, 4)}, %[qrd] offset:{1024 * i}", "lds_rd", (), aset(A_Q + 4 * i, 4)))
+        q_reads = [Ins(f"ds_read_b128 {arng(A_Q + 4 * i, 4)}, %[qrd] offset:{1024 * i}", "lds_rd", (),
+                       aset(A_Q + 4 * i, 4)) for i in range(16)]
+        if not q16:
+            # (the previous unit's conversions wrote them and waited)
+            for x in q_reads:
+                e(x)
         for j, w in enumerate(("kw0", "kw1", "kw2", "rw3")):
             e(Ins(f"s_mov_b32 s{S_K + j}, %[{w}]", "salu"))
         for j, w in enumerate(("vw0", "vw1", "vw2", "rw3")):
@@ -1020,6 +1054,11 @@ def _xl_unit_methods():
         tr.label(".Lxl_w16_%=")
         tr.raw(f"s_waitcnt vmcnt({XL_STORES['b16']})")
         tr.label(".Lxl_go_%=")
+        if q16:
+            # the previous unit's fragment DMAs are older than the stores:
+            # the wait above has seen them land
+            for x in q_reads:
+                e(x)
         tr.raw("s_waitcnt lgkmcnt(0)")
         tr.lds = []
         tr.raw("s_barrier")
@@ -1093,10 +1132,10 @@ def write_unit(path):
     """kd_fa_xlong64_loop.inc: the unit block of fa_fwd_xlong64."""
     out = ["// Generated by gen_w64_loop.py from this directory; do not edit.",
            "// The per-unit block of fa_fwd_xlong64 (kd_fa_kernel.hip) as inline-asm text.", ""]
-    for T in ("bf16", "f16"):
-        lines = Gen(T).build_unit()
+    for T, q16 in (("bf16", False), ("f16", False), ("bf16", True), ("f16", True)):
+        lines = Gen(T).build_unit(q16)
         check_registers(lines, XL_S_FIRST, XL_S_LAST)
-        out.append(f"#define KD_XL64_UNIT_{T.upper()} \\")
+        out.append(f"#define KD_XL64_UNIT_{T.upper()}{'_Q16' if q16 else ''} \\")
         for ln in lines:
             out.append(f'    "{ln}\\n" \\')
         out.append('    ""')

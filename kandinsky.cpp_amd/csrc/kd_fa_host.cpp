@@ -281,11 +281,12 @@ static bool use_xres(const kdfa::Args &a, int op, const kd_fa_desc *d, bool k_on
     return true;
 }
 
-// Unmasked key sets past the LDS-resident kernel's with F32 Q (the node as
-// ops::attention hands it over: the text cross-attention of a long prompt,
-// and any longer unmasked node) go to the persistent kernel on the 64-row
-// loop, fa_fwd_xlong64, when K is read as stored, Q is neither rotated nor
-// normalised, the 64-row kernel's limits hold (the partial last tile's
+// Unmasked key sets past the LDS-resident kernel's (the text cross-attention
+// of a long prompt as ops::attention hands it over, with F32 Q, and any
+// longer unmasked node) go to the persistent kernel on the 64-row loop,
+// fa_fwd_xlong64, when K is read as stored, Q is neither rotated nor
+// normalised and is F32 or in K's type (then with a scale >= 0: it does not
+// negate 16-bit Q), the 64-row kernel's limits hold (the partial last tile's
 // weights, 31-bit K/V offsets) and a wave's 64 Q and O rows lie within
 // 31-bit offsets of its first row.  (It beats fa_fwd_w64, whose workgroups
 // load Q, run the key loop and store O in sequence, at every length
@@ -294,22 +295,22 @@ static bool use_xres(const kdfa::Args &a, int op, const kd_fa_desc *d, bool k_on
 // KD_FA_ROUTE_NO_XLONG64 routes them as if it did not exist,
 // KD_FA_ROUTE_NO_XLONG, KD_FA_ROUTE_NO_W64 and KD_FA_ROUTE_W64_SHORT keep
 // them off the persistent kernels (for comparisons).
-static bool use_xlong64(const kdfa::Args &a, bool k_on_load, int route) {
+static bool use_xlong64(const kdfa::Args &a, int op, bool k_on_load, int route) {
     if (route & (KD_FA_ROUTE_NO_XLONG | KD_FA_ROUTE_NO_XLONG64 | KD_FA_ROUTE_NO_W64 | KD_FA_ROUTE_W64_SHORT))
         return false;
     if (a.m || k_on_load || a.rope_mode != KD_FA_ROPE_NONE || a.qn_w) return false;
-    if (a.Lk <= kdfa::kXresMaxKeys || a.q_type != KD_FA_TYPE_F32 || !w64_tail_ok(a)) return false;
+    if (a.Lk <= kdfa::kXresMaxKeys || !w64_tail_ok(a)) return false;
+    if (a.q_type != KD_FA_TYPE_F32 && !(a.q_type == op && a.scale_log2 >= 0.0f)) return false;
     const int64_t lim = (int64_t)1 << 31;
     return (int64_t)(a.Lk - 1) * a.k_nb1 + 256 < lim && (int64_t)(a.Lk - 1) * a.v_nb1 + 256 < lim &&
            63 * a.q_nb1 + 512 < lim && 63 * a.o_nb2 + 512 < lim;
 }
 
-// The other unmasked key sets just past the LDS-resident kernel's (Q in K's
-// type, or F32 with scale 0 and a partial last tile) go to the persistent
-// kernel that streams K and V with the next query tile's Q loaded during the
-// key loop, fa_fwd_xlong, when K is read as stored, Q is neither rotated nor
-// normalised and is stored as F32 or in K's type, and a unit's Q rows lie
-// within 32-bit offsets of its first row.  KD_FA_ROUTE_NO_XLONG and
+// The other unmasked key sets of up to 1,024 keys (Q in K's type with a
+// negative scale, or scale 0 and a partial last tile) go to the persistent
+// kernel on the 32-row step, fa_fwd_xlong, when K is read as stored, Q is
+// neither rotated nor normalised and is stored as F32 or in K's type, and a
+// unit's Q rows lie within 32-bit offsets of its first row.  KD_FA_ROUTE_NO_XLONG and
 // KD_FA_ROUTE_NO_W64 route them to the 32-row kernel, KD_FA_ROUTE_W64_SHORT
 // to the 64-row one (for comparisons).
 static bool use_xlong(const kdfa::Args &a, int op, bool k_on_load, int route) {
@@ -681,7 +682,7 @@ int run(const kd_fa_desc *d, const kd_fa_rope *r, const kd_fa_qk_norm *n, void *
             a.m_live_nqb = (int32_t)((Lq + 31) / 32);
         }
         e = kdfa::launch_xres(a, T, hs);
-    } else if (use_xlong64(a, k_rope, route)) {
+    } else if (use_xlong64(a, T, k_rope, route)) {
         a.n_qt = (int32_t)((Lq + kdfa::kXlongRows - 1) / kdfa::kXlongRows);
         a.n_blocks = (int32_t)(a.n_qt * H * B);
         e = kdfa::launch_xlong64(a, T, hs);

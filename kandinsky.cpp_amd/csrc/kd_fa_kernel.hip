@@ -2130,7 +2130,10 @@ static hipError_t launch_w64_t(const Args &a, hipStream_t s) {
 // ---------------------------------------------------------------------------
 // fa_fwd_xlong64: the persistent long-prompt kernel on fa_fwd_w64's key loop,
 // for F32 Q (the text cross-attention as ops::attention hands it over:
-// src/core/ops.hpp:122-124, src/models/crossdit.hpp:198).
+// src/core/ops.hpp:122-124, src/models/crossdit.hpp:198) and Q in K's type
+// (Q16: its fragments are its rows' 16-byte chunks, DMA'd straight into the
+// fragment area; a negative scale, which load_q_frags applies by negating Q,
+// is not taken then).
 //
 // One 4-wave workgroup per CU walks units of 256 query rows of one (b, h),
 // as fa_fwd_xlong does (XCD-contiguous unit ranges, workgroup j of an XCD
@@ -2162,7 +2165,7 @@ constexpr int kX64Raw = 8192;
 constexpr int kX64Lds = 163840;
 static_assert(kX64RawOff + 4 * kX64Raw == kX64Lds, "LDS plan");
 
-template <typename T>
+template <typename T, bool Q16>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void fa_fwd_xlong64(Args a) {
     typedef Elem<T> E;
@@ -2225,8 +2228,12 @@ void fa_fwd_xlong64(Args a) {
     const uint32_t rawb = __builtin_amdgcn_readfirstlane(lds0 + kX64RawOff + wave * kX64Raw);
     const uint32_t rawdelta = __builtin_amdgcn_readfirstlane((uint32_t)(kX64RawOff - kX64QOff) - wave * 8192u);
     // the next unit's Q rows: lane l reads row 32 qb + l % 32 of its wave
-    const uint32_t qoff0 = (uint32_t)l32 * (uint32_t)a.q_nb1 + 32u * (uint32_t)hi;
+    // (F32: the 16-byte halves of its 32-byte chunk; 16-bit: its fragment's
+    // 16-byte chunk)
+    const uint32_t qoff0 = (uint32_t)l32 * (uint32_t)a.q_nb1 + (Q16 ? 16u : 32u) * (uint32_t)hi;
     const uint32_t qoff1 = qoff0 + 32u * (uint32_t)a.q_nb1;
+    const uint32_t qfb = __builtin_amdgcn_readfirstlane(lds0 + kX64QOff + wave * 16384);
+    const uint32_t qrow_bytes = Q16 ? 256u : 512u;
 
     const uint32_t rw3 = 0x00020000u;
     const uint32_t kw2 = __builtin_amdgcn_readfirstlane((uint32_t)(a.Lk - 1) * (uint32_t)a.k_nb1 + 256u);
@@ -2275,7 +2282,7 @@ void fa_fwd_xlong64(Args a) {
             const int q_valid = min(a.Lq - qrow, 64);
             nkw2 = kw2;
             nvw2 = vw2;
-            nqw2 = q_valid > 0 ? (uint32_t)(q_valid - 1) * (uint32_t)a.q_nb1 + 512u : 0u;
+            nqw2 = q_valid > 0 ? (uint32_t)(q_valid - 1) * (uint32_t)a.q_nb1 + qrow_bytes : 0u;
         }
         const uint32_t kw0 = res_lo(kb), kw1 = res_hi(kb), vw0 = res_lo(vb), vw1 = res_hi(vb);
         const uint32_t ow0 = res_lo(ob), ow1 = res_hi(ob);
@@ -2296,13 +2303,17 @@ void fa_fwd_xlong64(Args a) {
         [nkw1] "s"(nkw1), [nkw2] "s"(nkw2u), [nvw0] "s"(nvw0), [nvw1] "s"(nvw1), [nvw2] "s"(nvw2u),           \
         [nqw0] "s"(nqw0), [nqw1] "s"(nqw1), [nqw2] "s"(nqw2u), [ow0] "s"(ow0), [ow1] "s"(ow1),               \
         [ow2] "s"(ow2u), [o8] "s"(o8), [onb2] "s"(onb2), [ot] "s"(ot), [qsgn] "s"(qsgn), [rawb] "s"(rawb),     \
-        [rawdelta] "s"(rawdelta)
+        [rawdelta] "s"(rawdelta), [qfb] "s"(qfb)
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-        if constexpr (__is_same(T, __bf16))
+        if constexpr (__is_same(T, __bf16) && !Q16)
             asm volatile(KD_XL64_UNIT_BF16 : : KD_XL64_OPERANDS : KD_XL64_CLOBBERS);
-        else
+        else if constexpr (!Q16)
             asm volatile(KD_XL64_UNIT_F16 : : KD_XL64_OPERANDS : KD_XL64_CLOBBERS);
+        else if constexpr (__is_same(T, __bf16))
+            asm volatile(KD_XL64_UNIT_BF16_Q16 : : KD_XL64_OPERANDS : KD_XL64_CLOBBERS);
+        else
+            asm volatile(KD_XL64_UNIT_F16_Q16 : : KD_XL64_OPERANDS : KD_XL64_CLOBBERS);
 #pragma clang diagnostic pop
 #undef KD_XL64_OPERANDS
         if (!has_next) break;
@@ -2315,7 +2326,10 @@ template <typename T>
 static void launch_xlong64_t(const Args &a, hipStream_t s) {
     // at most one workgroup per CU (256), a multiple of the 8 XCDs
     const int g = a.n_blocks < 256 ? (a.n_blocks + 7) / 8 * 8 : 256;
-    hipLaunchKernelGGL((fa_fwd_xlong64<T>), dim3(g), dim3(256), 0, s, a);
+    if (a.q_type == KD_FA_TYPE_F32)
+        hipLaunchKernelGGL((fa_fwd_xlong64<T, false>), dim3(g), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((fa_fwd_xlong64<T, true>), dim3(g), dim3(256), 0, s, a);
 }
 
 hipError_t launch_xlong64(const Args &a, int kv_type, hipStream_t s) {

@@ -2,9 +2,10 @@
 calls with more than 256 keys whose K is read as stored and whose Q is
 neither rotated nor normalised -- the text cross-attention of a long prompt
 (src/models/crossdit.hpp:198, no mask; up to 512 prompt tokens,
-src/models/qwen_tokenizer.hpp:128,183-186): fa_fwd_xlong64 (F32 Q, the
-64-row loop, any number of keys) and fa_fwd_xlong (up to 1,024 keys: 16-bit
-Q, and F32 Q with scale 0 and a partial last tile).
+src/models/qwen_tokenizer.hpp:128,183-186): fa_fwd_xlong64 (the 64-row
+loop, any number of keys; F32 Q, or Q in K's type with a scale >= 0) and
+fa_fwd_xlong (up to 1,024 keys: 16-bit Q with a negative scale, and scale 0
+with a partial last tile).
 
 Each case runs through the C ABI as routed and with the kernels routed out
 (kd_fa_set_routing): KD_FA_ROUTE_NO_XLONG64 (fa_fwd_xlong, or fa_fwd_w64
@@ -117,13 +118,16 @@ def test_xlong_reference_form_full_size():
 
 
 @pytest.mark.parametrize("scale", [-0.0883883, 0.0, 2.0], ids=["neg", "zero", "large"])
-def test_xlong_scales(scale):
+@pytest.mark.parametrize("qt", [torch.float32, torch.float16], ids=["q32", "q16"])
+def test_xlong_scales(scale, qt):
     """Scores that grow key by key move the running max from tile to tile;
-    with scale 0 the keys of the partial tile must still get weight 0."""
+    with scale 0 the keys of the partial tile must still get weight 0.  A
+    negative scale negates Q: F32 Q in the 64-row kernel's conversion,
+    16-bit Q on the 32-row kernel (the 64-row one DMAs 16-bit Q as stored)."""
     _need_gpu()
-    _announce(f"xlong scale {scale}")
+    _announce(f"xlong scale {scale} q {qt}")
     B, H, Lq, Lk = 1, 2, 700, 330
-    q, k, v = qkv(B, H, Lq, Lk, torch.float16, seed=9, q_dtype=torch.float32)
+    q, k, v = qkv(B, H, Lq, Lk, torch.float16, seed=9, q_dtype=qt)
     k = (k.float() * torch.linspace(0.2, 3.0, Lk).view(1, 1, Lk, 1)).to(torch.float16)
     qg, kg, vg = q.to(DEV), k.to(DEV), v.to(DEV)
     out, ref = _both(lambda: kd_fa.flash_attn_ext(qg, kg, vg, scale=scale))
