@@ -763,15 +763,14 @@ def _xl_unit_methods():
         the piece DMAs issued after them (XL_PIECE_DMAS) stay in flight:
         the conversion a step later waits for them, so that their memory
         latency overlaps a whole step."""
-        w0, wd = f".Lxl_w0_{tag}_%=", f".Lxl_wd_{tag}_%="
-        self.piece_index(tr, toff)
-        tr.raw(f"s_cmp_lt_u32 s{S_T2}, {XL_PIECES}")
-        tr.raw(f"s_cbranch_scc0 {w0}")
-        tr.raw(f"s_waitcnt vmcnt({XL_Q16_DMAS if self.q16 else XL_PIECE_DMAS})")
-        tr.raw(f"s_branch {wd}")
-        tr.label(w0)
+        # (steps past the pieces fall through: one compare, no taken branch)
+        wp, wd = f".Lxl_wp_{tag}_%=", f".Lxl_wd_{tag}_%="
+        tr.raw(f"s_cmp_le_u32 s{S_T}, {XL_PIECES - 1 - toff}")
+        tr.raw(f"s_cbranch_scc1 {wp}")
         tr.raw("s_waitcnt vmcnt(0)")
         tr.label(wd)
+        self.slow.append([f"{wp}:", f"s_waitcnt vmcnt({XL_Q16_DMAS if self.q16 else XL_PIECE_DMAS})",
+                          f"s_branch {wd}"])
 
     def piece_block(self, tr, p, toff, tag):
         """In step t = S_T + toff, t <= 4: piece t - 1 of the next unit's Q
@@ -785,13 +784,27 @@ def _xl_unit_methods():
         score registers S[p]; it ends with no LDS operation pending, so the
         tracker may go on as on the path that skips it."""
         R = S_BASE[p]
-        skip, noconv = f".Lxl_nopiece_{tag}_%=", f".Lxl_noconv_{tag}_%="
+        skip = f".Lxl_nopiece_{tag}_%="
+        # out of line, entered in steps 0-4 (the others fall through); the
+        # body goes on a tracker of its own: it ends with no LDS operation
+        # pending and writes only registers dead at the return
+        body = f".Lxl_piece_{tag}_%="
+        tr.raw(f"s_cmp_le_u32 s{S_T}, {XL_PIECES - toff}")
+        tr.raw(f"s_cbranch_scc1 {body}")
+        tr.label(skip)
+        tb = Tracker()
+        tb.label(body)
         if self.q16:
-            self.piece_block_q16(tr, R, toff, tag)
-            return
+            self.piece_block_q16(tb, R, toff, tag)
+        else:
+            self.piece_block_f32(tb, R, toff, tag)
+        tb.raw(f"s_branch {skip}")
+        self.slow.append(tb.out)
+
+    def piece_block_f32(self, tr, R, toff, tag):
+        """piece_block's body for F32 Q."""
+        noconv, done = f".Lxl_noconv_{tag}_%=", f".Lxl_piecedone_{tag}_%="
         self.piece_index(tr, toff)
-        tr.raw(f"s_cmp_gt_u32 s{S_T2}, {XL_PIECES}")
-        tr.raw(f"s_cbranch_scc1 {skip}")
         tr.raw("s_waitcnt lgkmcnt(0)")
         tr.raw(f"s_cmp_eq_u32 s{S_T2}, 0")
         tr.raw(f"s_cbranch_scc1 {noconv}")
@@ -819,7 +832,7 @@ def _xl_unit_methods():
         tr.label(noconv)
         # DMA of piece t
         tr.raw(f"s_cmp_ge_u32 s{S_T2}, {XL_PIECES}")
-        tr.raw(f"s_cbranch_scc1 {skip}")
+        tr.raw(f"s_cbranch_scc1 {done}")
         tr.raw(f"s_lshl_b32 s{S_T2}, s{S_T2}, 7")
         for qb in range(2):
             for kk in range(2):
@@ -830,7 +843,7 @@ def _xl_unit_methods():
                     tr.raw(f"s_add_u32 m0, %[rawb], {1024 * i}")
                     tr.raw("s_nop 0")
                     tr.raw(f"buffer_load_dwordx4 {vr(R + 52 + i)}, s[{S_NQ}:{S_NQ + 3}], 0 offen lds")
-        tr.label(skip)
+        tr.label(done)
 
     def piece_block_q16(self, tr, R, toff, tag):
         """Q stored in the operand type: in step t <= 3 each wave DMAs the
@@ -840,10 +853,10 @@ def _xl_unit_methods():
         32 ks + 16 (l / 32)); nothing to convert.  Their DMAs stay in flight
         past the step's end (step_wait); the next unit's first wait, for the
         tiles issued after them, covers them."""
-        skip = f".Lxl_nopiece_{tag}_%="
+        done = f".Lxl_piecedone_{tag}_%="
         self.piece_index(tr, toff)
         tr.raw(f"s_cmp_ge_u32 s{S_T2}, {XL_PIECES}")
-        tr.raw(f"s_cbranch_scc1 {skip}")
+        tr.raw(f"s_cbranch_scc1 {done}")
         tr.raw(f"s_lshl_b32 s{S_T2}, s{S_T2}, 6")
         tr.raw(f"s_lshl_b32 s{S_T3}, s{S_T2}, 5")
         for qb in range(2):
@@ -855,7 +868,7 @@ def _xl_unit_methods():
                 tr.raw(f"s_add_u32 m0, m0, {1024 * (8 * qb + kk)}")
                 tr.raw("s_nop 0")
                 tr.raw(f"buffer_load_dwordx4 {vr(R + 52 + i)}, s[{S_NQ}:{S_NQ + 3}], 0 offen lds")
-        tr.label(skip)
+        tr.label(done)
 
     def epilogue(self, tr):
         """After the last step: V(0) of the next unit once every wave is
