@@ -709,7 +709,8 @@ class Gen:
 # fa_fwd_xlong64 (kd_fa_kernel.hip) runs the loop above once per unit of 256
 # query rows of one (b, h) and walks several units per workgroup; its block
 # adds, per unit, the next unit's Q (F32 rows brought in by DMA during the
-# first steps and rounded into the Q fragment area), the next unit's first
+# first steps and rounded into the Q fragment area; Q stored in the operand
+# type DMA'd into it as it is), the next unit's first
 # K/V tiles (issued by the last step and after it) and the O epilogue
 # (normalised rows staged in LDS, stored as whole 128-byte lines through a
 # buffer resource whose record count ends at the last valid row).
@@ -773,21 +774,14 @@ def _xl_unit_methods():
                           f"s_branch {wd}"])
 
     def piece_block(self, tr, p, toff, tag):
-        """In step t = S_T + toff, t <= 4: piece t - 1 of the next unit's Q
-        rows (t >= 1) from the raw area, rounded to the operand type (with
-        load_q_frags' sign for scale < 0) into the fragment area; then the
-        DMA of piece t (t <= 3) into the raw area, which the conversion's
-        reads have left.  Piece p of a row is its bytes 128 p .. +127 (k-steps
-        2 p and 2 p + 1); DMA instruction i = 4 qb + 2 kk + j of a piece puts
-        lane l's 16 bytes of row 32 qb + l % 32, bytes 128 p + 64 kk +
-        32 (l / 32) + 16 j, at raw + 1024 i + 16 l.  The block uses the dead
-        score registers S[p]; it ends with no LDS operation pending, so the
-        tracker may go on as on the path that skips it."""
+        """The next unit's Q work of step t = S_T + toff, out of line: steps
+        0-4 branch to it, the others fall through on one compare.  The body
+        (piece_block_f32 / piece_block_q16) uses the dead score registers
+        S[p] and the free SGPRs, goes on a tracker of its own, and ends with
+        no LDS operation pending, so the main tracker may go on as on the
+        path that skips it."""
         R = S_BASE[p]
         skip = f".Lxl_nopiece_{tag}_%="
-        # out of line, entered in steps 0-4 (the others fall through); the
-        # body goes on a tracker of its own: it ends with no LDS operation
-        # pending and writes only registers dead at the return
         body = f".Lxl_piece_{tag}_%="
         tr.raw(f"s_cmp_le_u32 s{S_T}, {XL_PIECES - toff}")
         tr.raw(f"s_cbranch_scc1 {body}")
@@ -802,7 +796,14 @@ def _xl_unit_methods():
         self.slow.append(tb.out)
 
     def piece_block_f32(self, tr, R, toff, tag):
-        """piece_block's body for F32 Q."""
+        """F32 Q, step t <= 4: piece t - 1 of the next unit's rows (t >= 1)
+        from the raw area, rounded to the operand type (with load_q_frags'
+        sign for scale < 0) into the fragment area; then the DMA of piece t
+        (t <= 3) into the raw area, which the conversion's reads have left.
+        Piece p of a row is its bytes 128 p .. +127 (k-steps 2 p and
+        2 p + 1); DMA instruction i = 4 qb + 2 kk + j of a piece puts lane
+        l's 16 bytes of row 32 qb + l % 32, bytes 128 p + 64 kk + 32 (l / 32)
+        + 16 j, at raw + 1024 i + 16 l."""
         noconv, done = f".Lxl_noconv_{tag}_%=", f".Lxl_piecedone_{tag}_%="
         self.piece_index(tr, toff)
         tr.raw("s_waitcnt lgkmcnt(0)")
@@ -851,8 +852,9 @@ def _xl_unit_methods():
         the fragment area (the fragment layout is the rows' 16-byte chunks:
         lane l of fragment (qb, ks) holds row 32 qb + l % 32, bytes
         32 ks + 16 (l / 32)); nothing to convert.  Their DMAs stay in flight
-        past the step's end (step_wait); the next unit's first wait, for the
-        tiles issued after them, covers them."""
+        past the step's end (step_wait); the next step's end waits for them,
+        or, for those of a unit's last step, the next unit's first wait, for
+        the tiles issued after them, which its Q reads follow."""
         done = f".Lxl_piecedone_{tag}_%="
         self.piece_index(tr, toff)
         tr.raw(f"s_cmp_ge_u32 s{S_T2}, {XL_PIECES}")
