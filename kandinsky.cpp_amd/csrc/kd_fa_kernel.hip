@@ -2146,11 +2146,13 @@ static hipError_t launch_w64_t(const Args &a, hipStream_t s) {
 //     which the next unit loads its fragments;
 //   * the next unit's K(0), K(1) fetched by the unit's last step and V(0)
 //     once every wave is done with the V buffers, before the O stores, so
-//     that the next unit waits for those three tiles but not for the stores
-//     (loads and stores complete in issue order);
+//     that the next unit's first wait is for those three tiles and not for
+//     the stores (loads and stores complete in issue order: the end of its
+//     first step, which waits for that step's tiles, waits for them);
 //   * the O epilogue in the block: O / l staged per 32 rows in the raw area
-//     and stored as whole 128-byte lines through a buffer resource that ends
-//     at the last valid row (rows past Lq are not written).
+//     and stored, non-temporal, as whole 128-byte lines through a buffer
+//     resource that ends at the last valid row (rows past Lq are not
+//     written).
 // Per row the arithmetic is fa_fwd_w64's (and so fa_fwd_d128's): the
 // results are bitwise equal.
 //
