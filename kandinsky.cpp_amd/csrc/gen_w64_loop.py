@@ -957,6 +957,13 @@ def _xl_unit_methods():
         tr.out.extend(tb.out[n0:])
         tr.label(".Lxl_oend_%=")
 
+    @staticmethod
+    def zero_o(e, regs):
+        """O's accumulators cleared for the next unit once read (the first
+        unit of a workgroup clears them in its prologue)."""
+        for r in regs:
+            e(Ins(f"v_accvgpr_write_b32 a{r}, 0", "accw", (), {f"a{r}"}))
+
     def store_f32(self, tr):
         """F32 O: per (query block, 32-column block) the 32 rows' 128-byte
         pieces staged, then read back 8 rows x 128 bytes per instruction and
@@ -974,6 +981,7 @@ def _xl_unit_methods():
             for g in range(4):
                 e(Ins(f"ds_write_b128 {vr(EP_STW)}, {vrng(va + 4 * g, 4)} offset:{32 * g}", "lds_wr",
                       vset(va + 4 * g, 4) | {vr(EP_STW)}, ()))
+            self.zero_o(e, [A_O + 64 * qb + 16 * dblk + i for i in range(16)])
             for jr in range(4):
                 e(Ins(f"ds_read_b128 {vrng(rb + 4 * jr, 4)}, {vr(EP_STR)} offset:{8 * XL_PITCH * jr}", "lds_rd",
                       {vr(EP_STR)}, vset(rb + 4 * jr, 4)))
@@ -995,6 +1003,7 @@ def _xl_unit_methods():
             for i in range(32):
                 e(valu(f"v_mul_f32 {vr(va + i)}, {vr(va + i)}, {vr(EP_INV[qb])}", {vr(va + i), vr(EP_INV[qb])},
                        {vr(va + i)}))
+            self.zero_o(e, [A_O + 64 * qb + 16 * (2 * dp + dd) + i for dd in range(2) for i in range(16)])
             for dd in range(2):
                 for g in range(4):
                     for h in range(2):
@@ -1026,8 +1035,13 @@ def _xl_unit_methods():
         for qb in range(2):
             e(valu(f"v_mov_b32 {vr(M[qb])}, 0xff800000", (), {vr(M[qb])}))
             e(valu(f"v_mov_b32 {vr(LH[qb])}, 0", (), {vr(LH[qb])}))
+        # O = 0: the previous unit's epilogue cleared it; the first unit of a
+        # workgroup clears it here
+        tr.raw("s_cmp_eq_u32 %[first], 0")
+        tr.raw("s_cbranch_scc1 .Lxl_ozero_%=")
         for i in range(128):
             e(Ins(f"v_accvgpr_write_b32 a{A_O + i}, 0", "accw", (), {f"a{A_O + i}"}))
+        tr.label(".Lxl_ozero_%=")
         q_reads = [Ins(f"ds_read_b128 {arng(A_Q + 4 * i, 4)}, %[qrd] offset:{1024 * i}", "lds_rd", (),
                        aset(A_Q + 4 * i, 4)) for i in range(16)]
         if not q16:
