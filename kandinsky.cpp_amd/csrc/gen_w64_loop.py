@@ -777,9 +777,10 @@ def _xl_unit_methods():
         """The next unit's Q work of step t = S_T + toff, out of line: steps
         0-4 branch to it, the others fall through on one compare.  The body
         (piece_block_f32 / piece_block_q16) uses the dead score registers
-        S[p] and the free SGPRs, goes on a tracker of its own, and ends with
-        no LDS operation pending, so the main tracker may go on as on the
-        path that skips it."""
+        S[p] and the free SGPRs and goes on a tracker of its own; the main
+        tracker goes on as on the path that skips it: the body's LDS
+        operations left pending are fragment writes, older than any LDS
+        operation a later wait is for."""
         R = S_BASE[p]
         skip = f".Lxl_nopiece_{tag}_%="
         body = f".Lxl_piece_{tag}_%="
@@ -819,6 +820,7 @@ def _xl_unit_methods():
         for i in range(8):
             tr.raw(f"ds_read_b128 {vrng(R + 4 * i, 4)}, {vr(R + 32)} offset:{1024 * i}")
         tr.raw("s_waitcnt lgkmcnt(0)")
+        frags = []
         for qb in range(2):
             for kk in range(2):
                 j0, j1 = R + 4 * (4 * qb + 2 * kk), R + 4 * (4 * qb + 2 * kk + 1)
@@ -826,10 +828,22 @@ def _xl_unit_methods():
                 srcs = ((j0, j0 + 1), (j0 + 2, j0 + 3), (j1, j1 + 1), (j1 + 2, j1 + 3))
                 for x, (a, b) in enumerate(srcs):
                     tr.raw(f"{self.cvt} {vr(w + x)}, {vr(a)}, {vr(b)}")
-                for x in range(4):
-                    tr.raw(f"v_xor_b32 {vr(w + x)}, %[qsgn], {vr(w + x)}")
-                tr.raw(f"ds_write_b128 {vr(R + 33)}, {vrng(w, 4)} offset:{1024 * (8 * qb + kk)}")
-        tr.raw("s_waitcnt lgkmcnt(0)")
+                frags.append((w, 1024 * (8 * qb + kk)))
+        # scale < 0: Q negated (a sign XOR per element); never for the
+        # reference's positive scale
+        pos = f".Lxl_qpos_{tag}_%="
+        tr.raw("s_cmp_eq_u32 %[qsgn], 0")
+        tr.raw(f"s_cbranch_scc1 {pos}")
+        for w, _ in frags:
+            for x in range(4):
+                tr.raw(f"v_xor_b32 {vr(w + x)}, %[qsgn], {vr(w + x)}")
+        tr.label(pos)
+        for w, off in frags:
+            tr.raw(f"ds_write_b128 {vr(R + 33)}, {vrng(w, 4)} offset:{off}")
+        # (the fragment writes may still be pending at the return: LDS
+        # operations complete in order, so every later wait for a younger
+        # one waits for them too, and nothing before the next unit reads
+        # the fragment area)
         tr.label(noconv)
         # DMA of piece t
         tr.raw(f"s_cmp_ge_u32 s{S_T2}, {XL_PIECES}")
