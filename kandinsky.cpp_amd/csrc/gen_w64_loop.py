@@ -819,10 +819,12 @@ def _xl_unit_methods():
         tr.raw(f"v_add_u32 {vr(R + 33)}, s{S_T3}, %[qrd]")
         for i in range(8):
             tr.raw(f"ds_read_b128 {vrng(R + 4 * i, 4)}, {vr(R + 32)} offset:{1024 * i}")
-        tr.raw("s_waitcnt lgkmcnt(0)")
         frags = []
         for qb in range(2):
             for kk in range(2):
+                # this fragment's two reads have returned (LDS operations
+                # complete in order)
+                tr.raw(f"s_waitcnt lgkmcnt({6 - 2 * (2 * qb + kk)})")
                 j0, j1 = R + 4 * (4 * qb + 2 * kk), R + 4 * (4 * qb + 2 * kk + 1)
                 w = R + 36 + 4 * (2 * qb + kk)
                 srcs = ((j0, j0 + 1), (j0 + 2, j0 + 3), (j1, j1 + 1), (j1 + 2, j1 + 3))
