@@ -76,6 +76,7 @@ CASES = [
     (1, 2, 1, 1, 20, 600, torch.bfloat16, torch.float32),      # fewer rows than one wave's 32
     (1, 2, 2, 1, 700, 1500, torch.float16, torch.float32),     # past 1,024 keys: F32 Q only
     (2, 2, 1, 1, 333, 2113, torch.bfloat16, torch.float32),    # 34 tiles, GQA
+    (1, 3, 3, 1, 600, 1600, torch.float16, torch.float16),     # past 1,024 keys, Q in K's type
 ]
 
 
@@ -136,15 +137,16 @@ def test_xlong_scales(scale, qt):
                   f"xlong scale {scale}")
 
 
+@pytest.mark.parametrize("qt", [torch.float32, torch.bfloat16], ids=["q32", "q16"])
 @pytest.mark.parametrize("odt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
-def test_xlong_sixteen_bit_output(odt):
-    """16-bit dst: 8 store instructions per wave and unit (the count the
+def test_xlong_sixteen_bit_output(odt, qt):
+    """16-bit dst: 16 store instructions per wave and unit (the count the
     next unit's first wait leaves outstanding), equal to the F32 result
     rounded."""
     _need_gpu()
-    _announce(f"xlong 16-bit dst {odt}")
+    _announce(f"xlong 16-bit dst {odt} q {qt}")
     B, H, Lq, Lk = 2, 4, 1024, 450
-    q, k, v = qkv(B, H, Lq, Lk, torch.bfloat16, seed=17, q_dtype=torch.float32)
+    q, k, v = qkv(B, H, Lq, Lk, torch.bfloat16, seed=17, q_dtype=qt)
     qg, kg, vg = q.to(DEV), k.to(DEV), v.to(DEV)
     f32 = kd_fa.flash_attn_ext(qg, kg, vg)
     out, ref = _both(lambda: kd_fa.flash_attn_ext(qg, kg, vg, out_dtype=odt))
