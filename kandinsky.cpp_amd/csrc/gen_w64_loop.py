@@ -681,22 +681,9 @@ class Gen:
         tr.label(".Lw64_last0_%=")
         self.step(tr, 0, True, "e")
         tr.label(".Lw64_done_%=")
-        # O and the sums -> LDS (over K, V and Q, once every wave is done)
-        tr.raw("s_nop 7", 8)
-        tr.raw("s_nop 7", 8)
-        tr.raw("s_nop 7", 8)
-        tr.raw("s_barrier")
-        tr.mfma_w.clear()
-        for qb in range(2):
-            for dblk in range(4):
-                for g in range(4):
-                    a = A_O + 64 * qb + 16 * dblk + 4 * g
-                    e(Ins(f"ds_write_b128 %[ord], {arng(a, 4)} offset:{((qb * 4 + dblk) * 4 + g) * 1024}", "lds_wr",
-                          aset(a, 4), ()))
-        # the half-row sums
-        for qb in range(2):
-            e(Ins(f"ds_write_b32 %[lrd], {vr(LH[qb])} offset:{256 * qb}", "lds_wr", {vr(LH[qb])}, ()))
-        tr.raw("s_waitcnt lgkmcnt(0)")
+        # O / l -> the rows, staged over the K/V tiles once every wave is
+        # done with them
+        self.epilogue(tr, next_v=False)
         tr.raw("s_branch .Lw64_end_%=")
         lines = tr.out
         for blk in self.slow:
@@ -888,18 +875,20 @@ def _xl_unit_methods():
                 tr.raw(f"buffer_load_dwordx4 {vr(R + 52 + i)}, s[{S_NQ}:{S_NQ + 3}], 0 offen lds")
         tr.label(done)
 
-    def epilogue(self, tr):
-        """After the last step: V(0) of the next unit once every wave is
-        done with the V buffers, then O / l of the unit's rows as whole
-        lines (store_o_row_l's arithmetic: l the sum over the lane pair,
-        O * (l == 0 ? 0 : 1 / l) with the correctly rounded division)."""
+    def epilogue(self, tr, next_v=True):
+        """After the last step, once every wave is done with the K/V
+        buffers: V(0) of the next unit (next_v), then O / l of the rows as
+        whole lines (store_o_row_l's arithmetic: l the sum over the lane
+        pair, O * (l == 0 ? 0 : 1 / l) with the correctly rounded
+        division), staged in the wave's 8 KiB at %[rawb]."""
         e = tr.emit
         tr.raw("s_barrier")
-        for j, w in enumerate(("nvw0", "nvw1", "nvw2", "rw3")):
-            e(Ins(f"s_mov_b32 s{S_V + j}, %[{w}]", "salu"))
-        for j in range(4):
-            for x in self.dma("v", VBUF[0], j):
-                e(x)
+        if next_v:
+            for j, w in enumerate(("nvw0", "nvw1", "nvw2", "rw3")):
+                e(Ins(f"s_mov_b32 s{S_V + j}, %[{w}]", "salu"))
+            for j in range(4):
+                for x in self.dma("v", VBUF[0], j):
+                    e(x)
         t = EP_T
         for qb in range(2):
             e(valu(f"v_mov_b32 {vr(X)}, {vr(LH[qb])}", {vr(LH[qb])}, {vr(X)}))
@@ -942,8 +931,8 @@ def _xl_unit_methods():
         e(valu(f"v_mul_lo_u32 {a0}, %[onb2], {a0}", {a0}, {a0}))
         e(valu(f"v_lshl_add_u32 {vr(EP_OOFF)}, {a1}, 4, {a0}", {a1, a0}, {vr(EP_OOFF)}))
         for k in range(8):
-            tr.raw(f"s_mul_i32 s{S_T2}, %[o8], {k}")
-            e(valu(f"v_add_u32 {vr(EP_OROW[k])}, s{S_T2}, {vr(EP_OOFF)}", {vr(EP_OOFF)}, {vr(EP_OROW[k])}))
+            tr.raw(f"s_mul_i32 s{S_TMP}, %[o8], {k}")
+            e(valu(f"v_add_u32 {vr(EP_OROW[k])}, s{S_TMP}, {vr(EP_OOFF)}", {vr(EP_OOFF)}, {vr(EP_OROW[k])}))
         for j, w in enumerate(("ow0", "ow1", "ow2", "rw3")):
             e(Ins(f"s_mov_b32 s{S_K + j}, %[{w}]", "salu"))
         # every MFMA result has settled before the paths below read O
@@ -973,10 +962,12 @@ def _xl_unit_methods():
         tr.out.extend(tb.out[n0:])
         tr.label(".Lxl_oend_%=")
 
-    @staticmethod
-    def zero_o(e, regs):
-        """O's accumulators cleared for the next unit once read (the first
-        unit of a workgroup clears them in its prologue)."""
+    def zero_o(self, e, regs):
+        """In the persistent kernel's block, O's accumulators cleared for the
+        next unit once read (the first unit of a workgroup clears them in
+        its prologue)."""
+        if not getattr(self, "clear_o", False):
+            return
         for r in regs:
             e(Ins(f"v_accvgpr_write_b32 a{r}, 0", "accw", (), {f"a{r}"}))
 
@@ -1046,6 +1037,7 @@ def _xl_unit_methods():
         those (the previous unit's O stores, issued after them, complete in
         issue order)."""
         self.q16 = q16
+        self.clear_o = True
         tr = Tracker()
         e = tr.emit
         for qb in range(2):

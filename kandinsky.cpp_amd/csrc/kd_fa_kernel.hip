@@ -1913,13 +1913,13 @@ hipError_t launch_mask_live(const Args &a, uint32_t *out, hipStream_t stream) {
 // any softmax reads them, which gives them fa_fwd_d128's tail weights (0)
 // and row max (the valid keys').
 // LDS: K and V tiles double-buffered (0 .. 64 KiB), the Q fragments handed
-// to the loop (64 .. 128 KiB); after the loop, O (0 .. 128 KiB) and the row
-// sums (128 .. 130 KiB) handed back.
+// to the loop (64 .. 128 KiB).  The loop ends by storing O / l itself: each
+// wave stages its rows in 8 KiB over the K/V tiles and stores whole 128-byte
+// lines through a buffer resource that ends at the last valid row.
 #include "kd_fa_w64_loop.inc"
 
-constexpr int kW64Lds = 135168;
+constexpr int kW64Lds = 131072;
 constexpr int kW64QOff = 65536;
-constexpr int kW64LOff = 131072;   // half-row sums
 
 template <typename T, int RM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -1979,9 +1979,21 @@ void fa_fwd_w64(Args a) {
         vdma[j] = (uint32_t)(r0 + 16 * j) * (uint32_t)a.v_nb1 + ((pc ^ v_swz(r0)) << 4);
     }
     const uint32_t qrd = lds0 + kW64QOff + wave * 16384 + lane * 16;
-    const uint32_t ord = lds0 + wave * 32768 + lane * 16;
-    const uint32_t lrd = lds0 + kW64LOff + wave * 512 + lane * 4;
     const uint32_t dmab = __builtin_amdgcn_readfirstlane(lds0 + wave * 1024);
+    // O: this wave's 64 rows from a buffer resource whose record count ends
+    // at the last valid row (0 when none is), staged per wave in 8 KiB of the
+    // K/V tiles
+    const uint32_t rawb = __builtin_amdgcn_readfirstlane(lds0 + wave * 8192);
+    const uint32_t ot = a.o_type == KD_FA_TYPE_F32 ? 0u : a.o_type == KD_FA_TYPE_BF16 ? 1u : 2u;
+    const uint32_t onb2 = (uint32_t)a.o_nb2;
+    const uint32_t o8 = 8u * onb2;
+    const int orow = qt * 256 + wave * 64;
+    const char *ob = a.o + (int64_t)b * a.o_nb3 + (int64_t)h * a.o_nb1 + (int64_t)orow * a.o_nb2;
+    const int o_valid = min(a.Lq - orow, 64);
+    const uint32_t ow0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)ob);
+    const uint32_t ow1 = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)(uintptr_t)ob >> 32) & 0xffffu);
+    const uint32_t ow2 = __builtin_amdgcn_readfirstlane(
+        o_valid > 0 ? (uint32_t)(o_valid - 1) * onb2 + (ot == 0 ? 512u : 256u) : 0u);
 
     // buffer resources of this head's K and V: base, no stride, records up to
     // the end of key Lk-1, raw dword access
@@ -2012,10 +2024,11 @@ void fa_fwd_w64(Args a) {
         [krd5] "v"(krd[5]), [krd6] "v"(krd[6]), [krd7] "v"(krd[7]), [vrd0] "v"(vrd[0]), [vrd1] "v"(vrd[1]), \
         [vrd2] "v"(vrd[2]), [vrd3] "v"(vrd[3]), [kdma0] "v"(kdma[0]), [kdma1] "v"(kdma[1]),                \
         [kdma2] "v"(kdma[2]), [kdma3] "v"(kdma[3]), [vdma0] "v"(vdma[0]), [vdma1] "v"(vdma[1]),            \
-        [vdma2] "v"(vdma[2]), [vdma3] "v"(vdma[3]), [qrd] "v"(qrd), [ord] "v"(ord), [lrd] "v"(lrd),        \
-        [kw0] "s"(kw0), [kw1] "s"(kw1), [kw2] "s"(kw2), [kw3] "s"(rw3), [vw0] "s"(vw0), [vw1] "s"(vw1),    \
-        [vw2] "s"(vw2), [vw3] "s"(rw3), [ktile] "s"(ktile), [vtile] "s"(vtile), [n] "s"(n_tiles),          \
-        [c2] "s"(c2), [dmab] "s"(dmab), [mstep] "s"(mstep), [thr] "v"(thr)
+        [vdma2] "v"(vdma[2]), [vdma3] "v"(vdma[3]), [qrd] "v"(qrd), [kw0] "s"(kw0), [kw1] "s"(kw1),        \
+        [kw2] "s"(kw2), [kw3] "s"(rw3), [vw0] "s"(vw0), [vw1] "s"(vw1), [vw2] "s"(vw2), [vw3] "s"(rw3),    \
+        [rw3] "s"(rw3), [ktile] "s"(ktile), [vtile] "s"(vtile), [n] "s"(n_tiles), [c2] "s"(c2),              \
+        [dmab] "s"(dmab), [mstep] "s"(mstep), [thr] "v"(thr), [rawb] "s"(rawb), [ow0] "s"(ow0),             \
+        [ow1] "s"(ow1), [ow2] "s"(ow2), [o8] "s"(o8), [onb2] "s"(onb2), [ot] "s"(ot)
 // (m0 is in the clobber list for the reader; the compiler reserves it and
 // uses it nowhere in this kernel)
 #pragma clang diagnostic push
@@ -2026,89 +2039,6 @@ void fa_fwd_w64(Args a) {
         asm volatile(KD_W64_LOOP_F16 : : KD_W64_OPERANDS : KD_W64_CLOBBERS);
 #pragma clang diagnostic pop
 #undef KD_W64_OPERANDS
-    __syncthreads();
-
-    // O and the half-row sums from LDS
-    f32x16 o[2][4];
-    float l_half[2];
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-#pragma unroll
-        for (int dblk = 0; dblk < 4; ++dblk)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const f32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) f32x4 *>(
-                    lds + wave * 32768 + ((qb * 4 + dblk) * 4 + g) * 1024 + lane * 16);
-                o[qb][dblk][4 * g] = v.x;
-                o[qb][dblk][4 * g + 1] = v.y;
-                o[qb][dblk][4 * g + 2] = v.z;
-                o[qb][dblk][4 * g + 3] = v.w;
-            }
-        l_half[qb] = *reinterpret_cast<const __attribute__((address_space(3))) float *>(
-            lds + kW64LOff + wave * 512 + qb * 256 + lane * 4);
-    }
-
-    // O / l -> the rows as whole 128-byte lines (store_o_row_l's arithmetic).
-    // Each wave stages its 64 rows in its own 32 KiB of LDS, row-major with
-    // the 16-byte chunk index XOR the row's low bits (no bank conflicts);
-    // then lane L stores chunk L%32 of row 2j + L/32 (16-bit O: chunk L%16 of
-    // row 4j + L/16), so that each store instruction writes whole lines of
-    // two (four) rows instead of 32-byte pieces of 32 rows, which the memory
-    // wrote as separate partial lines.
-    {
-        lds_t *const stage = lds + wave * 32768;
-        const bool f32o = a.o_type == KD_FA_TYPE_F32;
-        const bool bfo = a.o_type == KD_FA_TYPE_BF16;
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-            const float l_run = pair_sum(l_half[qb]);
-            const float inv = l_run == 0.0f ? 0.0f : 1.0f / l_run;
-            const int r = qb * 32 + l32;
-#pragma unroll
-            for (int dblk = 0; dblk < 4; ++dblk)
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const f32x4 v = {o[qb][dblk][4 * g] * inv, o[qb][dblk][4 * g + 1] * inv,
-                                     o[qb][dblk][4 * g + 2] * inv, o[qb][dblk][4 * g + 3] * inv};
-                    if (f32o) {
-                        const int c = dblk * 8 + 2 * g + hi;
-                        *reinterpret_cast<__attribute__((address_space(3))) f32x4 *>(
-                            stage + r * 512 + ((c ^ (r & 31)) << 4)) = v;
-                    } else {
-                        const u32x2 w = bfo ? (u32x2){Elem<__bf16>::pack2(v.x, v.y), Elem<__bf16>::pack2(v.z, v.w)}
-                                            : (u32x2){Elem<_Float16>::pack2(v.x, v.y), Elem<_Float16>::pack2(v.z, v.w)};
-                        const int c = dblk * 4 + g;
-                        *reinterpret_cast<__attribute__((address_space(3))) u32x2 *>(
-                            stage + r * 256 + ((c ^ (r & 15)) << 4) + 8 * hi) = w;
-                    }
-                }
-        }
-        // (LDS operations of a wave complete in order: the reads below see
-        // the writes above)
-        char *const obase = a.o + (int64_t)b * a.o_nb3 + (int64_t)h * a.o_nb1;
-        const int row0 = qt * 256 + wave * 64;
-        const int64_t o_nb2 = a.o_nb2;
-        const int Lq = a.Lq;
-        if (f32o) {
-#pragma unroll 8
-            for (int j = 0; j < 32; ++j) {
-                const int r = 2 * j + (lane >> 5);
-                const int c = lane & 31;
-                const u32x4 w = *reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(
-                    stage + r * 512 + ((c ^ (r & 31)) << 4));
-                if (row0 + r < Lq) *reinterpret_cast<u32x4 *>(obase + (int64_t)(row0 + r) * o_nb2 + c * 16) = w;
-            }
-        } else {
-#pragma unroll 8
-            for (int j = 0; j < 16; ++j) {
-                const int r = 4 * j + (lane >> 4);
-                const int c = lane & 15;
-                const u32x4 w = *reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(
-                    stage + r * 256 + ((c ^ (r & 15)) << 4));
-                if (row0 + r < Lq) *reinterpret_cast<u32x4 *>(obase + (int64_t)(row0 + r) * o_nb2 + c * 16) = w;
-            }
-        }
-    }
 }
 
 template <typename T>
