@@ -1,6 +1,10 @@
 #!/usr/bin/env python3
 """Writes kd_fa_w64_loop.inc: the key loop of fa_fwd_w64 (64 query rows per
-wave, one wave per SIMD) as inline-asm strings, one per operand type.
+wave, one wave per SIMD) as inline-asm strings, one per operand type, from
+the Q fragments in LDS to O / l stored as whole lines; and
+kd_fa_xlong64_loop.inc: fa_fwd_xlong64's per-unit block, the same loop for
+one unit of a persistent workgroup with the next unit's Q and first K / V
+tiles brought in during it.
 
 The loop is scheduled by hand because its two ingredients need registers
 that the compiler does not give it: O (64 rows x 128 floats per wave = 128
@@ -16,6 +20,11 @@ another tile of the same wave.  Per 64-key tile t (step t):
             the last MFMAs of phase 1, the branch after the last one
   phase 2   MFMA  O^T += V(t)^T P(t)^T       32 x 32x32x16, V^T by ds_read_b64_tr_b16
             VALU  softmax of S(t+1), keys 0-31
+
+After the last tile, the epilogue: l summed over the lane pair, 1 / l by
+the correctly rounded division sequence, O / l staged per 32 rows and 32
+columns over the K / V tiles and stored 8 rows x 128 bytes per instruction
+through a buffer resource that ends at the last valid row.
 
 A partial last tile (Lk not a multiple of 64) runs in the loop like the
 others: its K and V rows past Lk read zeros (the buffer resources end at key
