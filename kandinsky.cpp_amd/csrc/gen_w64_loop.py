@@ -621,6 +621,32 @@ class Gen:
         else:
             self.merge(tr, vseq, [])
 
+    def first_tiles(self, e, dma):
+        """The K and V resources from the operands, moved past K(0), V(0)
+        and K(1) -- with dma, also the DMAs of those tiles (a DMA past the
+        last tile reads zeros: the resource's record count is clamped at
+        0)."""
+        for j, w in enumerate(("kw0", "kw1", "kw2", "kw3")):
+            e(Ins(f"s_mov_b32 s{S_K + j}, %[{w}]", "salu"))
+        for j, w in enumerate(("vw0", "vw1", "vw2", "vw3")):
+            e(Ins(f"s_mov_b32 s{S_V + j}, %[{w}]", "salu"))
+        for which, buf in (("k", KBUF[0]), ("v", VBUF[0]), ("k", KBUF[1])):
+            if dma:
+                for j in range(4):
+                    for x in self.dma(which, buf, j):
+                        e(x)
+            for x in self.advance(which):
+                e(x)
+
+    def build_pre(self):
+        """The block fa_fwd_w64 runs before its Q loads: the DMAs of K(0),
+        V(0) and K(1), so that their round trip overlaps the Q load's (the
+        kernel's wait for its Q loads, which come later in the same in-order
+        counter, covers them)."""
+        tr = Tracker()
+        self.first_tiles(tr.emit, dma=True)
+        return tr.out
+
     def build(self):
         tr = Tracker()
         e = tr.emit
@@ -631,27 +657,9 @@ class Gen:
             e(Ins(f"v_accvgpr_write_b32 a{A_O + i}, 0", "accw", (), {f"a{A_O + i}"}))
         for i in range(16):
             e(Ins(f"ds_read_b128 {arng(A_Q + 4 * i, 4)}, %[qrd] offset:{1024 * i}", "lds_rd", (), aset(A_Q + 4 * i, 4)))
-        for j, w in enumerate(("kw0", "kw1", "kw2", "kw3")):
-            e(Ins(f"s_mov_b32 s{S_K + j}, %[{w}]", "salu"))
-        for j, w in enumerate(("vw0", "vw1", "vw2", "vw3")):
-            e(Ins(f"s_mov_b32 s{S_V + j}, %[{w}]", "salu"))
-        # K(0), V(0), K(1) (a DMA past the last tile reads zeros: the
-        # resource's record count is clamped at 0)
-        for j in range(4):
-            for x in self.dma("k", KBUF[0], j):
-                e(x)
-        for x in self.advance("k"):
-            e(x)
-        for j in range(4):
-            for x in self.dma("v", VBUF[0], j):
-                e(x)
-        for x in self.advance("v"):
-            e(x)
-        for j in range(4):
-            for x in self.dma("k", KBUF[1], j):
-                e(x)
-        for x in self.advance("k"):
-            e(x)
+        # K(0), V(0), K(1) were issued by build_pre's block, ahead of the
+        # kernel's Q loads; here the resources only move past them
+        self.first_tiles(e, dma=False)
         tr.raw("s_waitcnt vmcnt(0) lgkmcnt(0)")
         tr.lds = []
         tr.raw("s_barrier")
@@ -1213,6 +1221,17 @@ def main(path=None, kpre=2, vpre=2, per1=4, check_at=29, check_spread=True):
             out.append(f'    "{ln}\\n" \\')
         out.append('    ""')
         out.append("")
+    pre = Gen("bf16").build_pre()
+    check_registers(pre)
+    out.append("#define KD_W64_PRE \\")
+    for ln in pre:
+        out.append(f'    "{ln}\\n" \\')
+    out.append('    ""')
+    out.append("")
+    out.append("#define KD_W64_PRE_CLOBBERS \\")
+    out.append("    " + ", ".join(f'"s{S_K + j}"' for j in range(4)) + ", " +
+               ", ".join(f'"s{S_V + j}"' for j in range(4)) + ', "scc", "m0", "memory"')
+    out.append("")
     out.append("#define KD_W64_CLOBBERS \\")
     regs = [f'"v{i}"' for i in range(24, V_LAST + 1)] + [f'"a{i}"' for i in range(A_LAST + 1)] + \
            [f'"s{i}"' for i in range(S_FIRST, S_LAST + 1)]

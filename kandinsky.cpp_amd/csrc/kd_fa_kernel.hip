@@ -1946,6 +1946,46 @@ void fa_fwd_w64(Args a) {
     const int h = bh % a.H;
     const int b = bh / a.H;
 
+    // DMA: round j of wave w fills tile rows 4*(w + 4j) .. +3 (1 KiB at
+    // LDS (w + 4j) * 1024); lane: row 4*(w + 4j) + lane/16, chunk lane%16
+    const int r0 = 4 * wave + (lane >> 4);
+    const int pc = lane & 15;
+    uint32_t kdma[4], vdma[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        kdma[j] = (uint32_t)(k_row_of(r0) + 16 * j) * (uint32_t)a.k_nb1 + ((pc ^ (r0 & 15)) << 4);
+        vdma[j] = (uint32_t)(r0 + 16 * j) * (uint32_t)a.v_nb1 + ((pc ^ v_swz(r0)) << 4);
+    }
+    const uint32_t dmab = __builtin_amdgcn_readfirstlane(lds0 + wave * 1024);
+    // buffer resources of this head's K and V: base, no stride, records up to
+    // the end of key Lk-1, raw dword access
+    const char *kbase = a.k + (int64_t)(h / a.rk2) * a.k_nb2 + (int64_t)(b / a.rk3) * a.k_nb3;
+    const char *vbase = a.v + (int64_t)(h / a.rv2) * a.v_nb2 + (int64_t)(b / a.rv3) * a.v_nb3;
+    const uint64_t ka = (uint64_t)(uintptr_t)kbase, va = (uint64_t)(uintptr_t)vbase;
+    const uint32_t kw0 = __builtin_amdgcn_readfirstlane((uint32_t)ka);
+    const uint32_t kw1 = __builtin_amdgcn_readfirstlane((uint32_t)(ka >> 32) & 0xffffu);
+    const uint32_t kw2 = __builtin_amdgcn_readfirstlane((uint32_t)(a.Lk - 1) * (uint32_t)a.k_nb1 + 256u);
+    const uint32_t vw0 = __builtin_amdgcn_readfirstlane((uint32_t)va);
+    const uint32_t vw1 = __builtin_amdgcn_readfirstlane((uint32_t)(va >> 32) & 0xffffu);
+    const uint32_t vw2 = __builtin_amdgcn_readfirstlane((uint32_t)(a.Lk - 1) * (uint32_t)a.v_nb1 + 256u);
+    const uint32_t rw3 = 0x00020000u;
+    const uint32_t ktile = __builtin_amdgcn_readfirstlane(64u * (uint32_t)a.k_nb1);
+    const uint32_t vtile = __builtin_amdgcn_readfirstlane(64u * (uint32_t)a.v_nb1);
+    // K(0), V(0) and K(1) by DMA ahead of the Q loads, so that the two round
+    // trips overlap (the wait for Q, later in the same in-order counter,
+    // covers them; the tiles land below the Q fragments' LDS)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+    asm volatile(KD_W64_PRE
+                 :
+                 : [kdma0] "v"(kdma[0]), [kdma1] "v"(kdma[1]), [kdma2] "v"(kdma[2]), [kdma3] "v"(kdma[3]),
+                   [vdma0] "v"(vdma[0]), [vdma1] "v"(vdma[1]), [vdma2] "v"(vdma[2]), [vdma3] "v"(vdma[3]),
+                   [dmab] "s"(dmab), [kw0] "s"(kw0), [kw1] "s"(kw1), [kw2] "s"(kw2), [kw3] "s"(rw3),
+                   [vw0] "s"(vw0), [vw1] "s"(vw1), [vw2] "s"(vw2), [vw3] "s"(rw3), [ktile] "s"(ktile),
+                   [vtile] "s"(vtile)
+                 : KD_W64_PRE_CLOBBERS);
+#pragma clang diagnostic pop
+
     // Q fragments of the wave's two 32-row blocks -> LDS, lane-major
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
@@ -1968,18 +2008,7 @@ void fa_fwd_w64(Args a) {
 #pragma unroll
     for (int dblk = 0; dblk < 4; ++dblk)
         vrd[dblk] = lds0 + 2048 * hi + 256 * v_sub + (((4 * dblk + v_c_lo) ^ v_swz(v_sub)) << 4) + 8 * (lane & 1);
-    // DMA: round j of wave w fills tile rows 4*(w + 4j) .. +3 (1 KiB at
-    // LDS (w + 4j) * 1024); lane: row 4*(w + 4j) + lane/16, chunk lane%16
-    const int r0 = 4 * wave + (lane >> 4);
-    const int pc = lane & 15;
-    uint32_t kdma[4], vdma[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        kdma[j] = (uint32_t)(k_row_of(r0) + 16 * j) * (uint32_t)a.k_nb1 + ((pc ^ (r0 & 15)) << 4);
-        vdma[j] = (uint32_t)(r0 + 16 * j) * (uint32_t)a.v_nb1 + ((pc ^ v_swz(r0)) << 4);
-    }
     const uint32_t qrd = lds0 + kW64QOff + wave * 16384 + lane * 16;
-    const uint32_t dmab = __builtin_amdgcn_readfirstlane(lds0 + wave * 1024);
     // O: this wave's 64 rows from a buffer resource whose record count ends
     // at the last valid row (0 when none is), staged per wave in 8 KiB of the
     // K/V tiles
@@ -1995,20 +2024,6 @@ void fa_fwd_w64(Args a) {
     const uint32_t ow2 = __builtin_amdgcn_readfirstlane(
         o_valid > 0 ? (uint32_t)(o_valid - 1) * onb2 + (ot == 0 ? 512u : 256u) : 0u);
 
-    // buffer resources of this head's K and V: base, no stride, records up to
-    // the end of key Lk-1, raw dword access
-    const char *kbase = a.k + (int64_t)(h / a.rk2) * a.k_nb2 + (int64_t)(b / a.rk3) * a.k_nb3;
-    const char *vbase = a.v + (int64_t)(h / a.rv2) * a.v_nb2 + (int64_t)(b / a.rv3) * a.v_nb3;
-    const uint64_t ka = (uint64_t)(uintptr_t)kbase, va = (uint64_t)(uintptr_t)vbase;
-    const uint32_t kw0 = __builtin_amdgcn_readfirstlane((uint32_t)ka);
-    const uint32_t kw1 = __builtin_amdgcn_readfirstlane((uint32_t)(ka >> 32) & 0xffffu);
-    const uint32_t kw2 = __builtin_amdgcn_readfirstlane((uint32_t)(a.Lk - 1) * (uint32_t)a.k_nb1 + 256u);
-    const uint32_t vw0 = __builtin_amdgcn_readfirstlane((uint32_t)va);
-    const uint32_t vw1 = __builtin_amdgcn_readfirstlane((uint32_t)(va >> 32) & 0xffffu);
-    const uint32_t vw2 = __builtin_amdgcn_readfirstlane((uint32_t)(a.Lk - 1) * (uint32_t)a.v_nb1 + 256u);
-    const uint32_t rw3 = 0x00020000u;
-    const uint32_t ktile = __builtin_amdgcn_readfirstlane(64u * (uint32_t)a.k_nb1);
-    const uint32_t vtile = __builtin_amdgcn_readfirstlane(64u * (uint32_t)a.v_nb1);
     // every tile, a partial last one included: the loop sets the scores of
     // its keys past Lk to -inf in step mstep (= n - 2; none when the last
     // tile is whole), against thr = its valid keys - 8 * (lane / 32)
